@@ -1,0 +1,328 @@
+// Device layer of libkvpersist.so: memory, copies and the arena staging
+// (compaction) kernels that replace the reference's per-row
+// cudaMemcpyAsync pairs (reference: src/kv_tile_manager.cu:104-121,
+// :153-192). One flush = (optional) KVMap rebuild + ONE gather launch that
+// moves every pending K|V row of the step into the arena.
+//
+// Gather kernel: one workgroup per staged row; the K bytes then the V bytes
+// land back to back at arena + dst_row * row_stride (the reference's
+// [K half | V half] row format). 16-byte vector moves when source, target and
+// sizes are 16-byte aligned, byte moves otherwise. The map scatter rides in
+// trailing workgroups of the same launch.
+//
+// Descriptors travel through a pinned-host / device ring: each flush copies
+// its descriptors H2D asynchronously on the caller's stream; a ring region is
+// reused only after the event recorded behind its last user has completed.
+
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdint>
+#include <cstdio>
+#include <cstring>
+#include <string>
+#include <vector>
+
+#include "kvp_c_api.h"
+#include "kvp_internal.h"
+
+namespace kvp {
+
+namespace {
+thread_local std::string g_last_error;
+void* g_stream = nullptr;
+}  // namespace
+
+void set_error(const char* fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    g_last_error = buf;
+}
+
+void clear_error() { g_last_error.clear(); }
+
+void* library_stream() { return g_stream; }
+
+namespace {
+
+constexpr int kStageThreads = 256;
+constexpr int kMapThreads = 256;
+
+__global__ __launch_bounds__(256) void map_fill_kernel(long* __restrict__ map, long n) {
+    const long stride = (long)gridDim.x * blockDim.x;
+    for (long i = (long)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) map[i] = -1L;
+}
+
+__device__ __forceinline__ void copy_bytes(unsigned char* __restrict__ dst,
+                                           const unsigned char* __restrict__ src,
+                                           unsigned bytes) {
+    typedef __attribute__((ext_vector_type(4))) unsigned int u32x4;
+    if ((((uintptr_t)dst | (uintptr_t)src | (uintptr_t)bytes) & 15u) == 0) {
+        const unsigned n16 = bytes >> 4;
+        const u32x4* s = reinterpret_cast<const u32x4*>(src);
+        u32x4* d = reinterpret_cast<u32x4*>(dst);
+        for (unsigned i = threadIdx.x; i < n16; i += blockDim.x) d[i] = s[i];
+    } else {
+        for (unsigned i = threadIdx.x; i < bytes; i += blockDim.x) dst[i] = src[i];
+    }
+}
+
+// blocks [0, n_copies): one row copy each; blocks after that: map scatter.
+__global__ __launch_bounds__(256) void stage_kernel(const KvpRowCopy* __restrict__ copies,
+                                                    long n_copies,
+                                                    unsigned char* __restrict__ arena,
+                                                    long row_stride,
+                                                    const long* __restrict__ map_rows,
+                                                    const long* __restrict__ map_slots,
+                                                    long n_map, long* __restrict__ map) {
+    const long b = blockIdx.x;
+    if (b < n_copies) {
+        const KvpRowCopy c = copies[b];
+        unsigned char* dst = arena + c.dst_row * row_stride;
+        copy_bytes(dst, static_cast<const unsigned char*>(c.k_src), c.k_bytes);
+        copy_bytes(dst + c.k_bytes, static_cast<const unsigned char*>(c.v_src), c.v_bytes);
+    } else {
+        const long i = (b - n_copies) * blockDim.x + threadIdx.x;
+        if (i < n_map) map[map_rows[i]] = map_slots[i];
+    }
+}
+
+struct Stager {
+    unsigned char* host = nullptr;
+    unsigned char* dev = nullptr;
+    size_t cap = 0;
+    size_t head = 0;
+    std::vector<hipEvent_t> inflight;
+    std::vector<hipEvent_t> spare;
+
+    ~Stager() {
+        drain();
+        for (hipEvent_t e : spare) (void)hipEventDestroy(e);
+        if (host) (void)hipHostFree(host);
+        if (dev) (void)hipFree(dev);
+    }
+    bool drain() {
+        bool ok = true;
+        for (hipEvent_t e : inflight) {
+            if (hipEventSynchronize(e) != hipSuccess) ok = false;
+            spare.push_back(e);
+        }
+        inflight.clear();
+        head = 0;
+        return ok;
+    }
+    bool reserve(size_t need) {
+        if (need > cap) {
+            if (!drain()) return false;
+            if (host) (void)hipHostFree(host);
+            if (dev) (void)hipFree(dev);
+            host = nullptr;
+            dev = nullptr;
+            size_t want = need < ((size_t)4 << 20) ? ((size_t)4 << 20) : need * 2;
+            if (hipHostMalloc(reinterpret_cast<void**>(&host), want, hipHostMallocDefault) != hipSuccess) {
+                host = nullptr;
+                cap = 0;
+                return false;
+            }
+            if (hipMalloc(reinterpret_cast<void**>(&dev), want) != hipSuccess) {
+                (void)hipHostFree(host);
+                host = nullptr;
+                dev = nullptr;
+                cap = 0;
+                return false;
+            }
+            cap = want;
+            head = 0;
+        }
+        if (head + need > cap) {
+            if (!drain()) return false;
+        }
+        return true;
+    }
+    hipEvent_t take_event() {
+        if (!spare.empty()) {
+            hipEvent_t e = spare.back();
+            spare.pop_back();
+            return e;
+        }
+        hipEvent_t e = nullptr;
+        if (hipEventCreateWithFlags(&e, hipEventDisableTiming) != hipSuccess) return nullptr;
+        return e;
+    }
+};
+
+size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
+
+}  // namespace
+}  // namespace kvp
+
+using kvp::set_error;
+
+extern "C" {
+
+const char* kvp_last_error(void) { return kvp::g_last_error.c_str(); }
+
+void kvp_set_stream(void* stream) { kvp::g_stream = stream; }
+void* kvp_get_stream(void) { return kvp::g_stream; }
+
+int kvp_device_count(void) {
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess) return 0;
+    return n;
+}
+
+void* kvp_dev_alloc(size_t bytes) {
+    void* p = nullptr;
+    if (bytes == 0) bytes = 1;
+    hipError_t e = hipMalloc(&p, bytes);
+    if (e != hipSuccess) {
+        set_error("hipMalloc(%zu): %s", bytes, hipGetErrorString(e));
+        return nullptr;
+    }
+    return p;
+}
+
+void kvp_dev_free(void* p) {
+    if (p) (void)hipFree(p);
+}
+
+int kvp_memcpy_h2d(void* dst, const void* src, size_t bytes, void* stream) {
+    hipError_t e = hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice,
+                                  static_cast<hipStream_t>(stream));
+    if (e == hipSuccess) e = hipStreamSynchronize(static_cast<hipStream_t>(stream));
+    if (e != hipSuccess) {
+        set_error("memcpy h2d: %s", hipGetErrorString(e));
+        return 1;
+    }
+    return 0;
+}
+
+int kvp_memcpy_d2h(void* dst, const void* src, size_t bytes, void* stream) {
+    hipError_t e = hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost,
+                                  static_cast<hipStream_t>(stream));
+    if (e == hipSuccess) e = hipStreamSynchronize(static_cast<hipStream_t>(stream));
+    if (e != hipSuccess) {
+        set_error("memcpy d2h: %s", hipGetErrorString(e));
+        return 1;
+    }
+    return 0;
+}
+
+int kvp_memcpy_d2d(void* dst, const void* src, size_t bytes, void* stream) {
+    hipError_t e = hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice,
+                                  static_cast<hipStream_t>(stream));
+    if (e != hipSuccess) {
+        set_error("memcpy d2d: %s", hipGetErrorString(e));
+        return 1;
+    }
+    return 0;
+}
+
+int kvp_stream_sync(void* stream) {
+    hipError_t e = hipStreamSynchronize(static_cast<hipStream_t>(stream));
+    if (e != hipSuccess) {
+        set_error("stream sync: %s", hipGetErrorString(e));
+        return 1;
+    }
+    return 0;
+}
+
+int kvp_device_sync(void) {
+    hipError_t e = hipDeviceSynchronize();
+    if (e != hipSuccess) {
+        set_error("device sync: %s", hipGetErrorString(e));
+        return 1;
+    }
+    return 0;
+}
+
+void* kvp_stager_create(void) { return new (std::nothrow) kvp::Stager(); }
+
+void kvp_stager_destroy(void* s) { delete static_cast<kvp::Stager*>(s); }
+
+int kvp_stage_run(void* stager, void* arena, long row_stride_bytes, const KvpRowCopy* copies,
+                  long n_copies, long* map_dev, long map_fill, const long* map_rows,
+                  const long* map_slots, long n_map, void* stream) {
+    kvp::Stager* st = static_cast<kvp::Stager*>(stager);
+    if (!st) {
+        set_error("stage: null stager");
+        return 1;
+    }
+    if (n_copies < 0 || n_map < 0 || map_fill < 0) {
+        set_error("stage: negative count");
+        return 1;
+    }
+    if (n_copies > 0 && (!arena || row_stride_bytes <= 0 || !copies)) {
+        set_error("stage: copies need an arena, a positive row stride and descriptors");
+        return 1;
+    }
+    if ((n_map > 0 || map_fill > 0) && !map_dev) {
+        set_error("stage: map entries without a device map");
+        return 1;
+    }
+    if (n_copies == 0 && n_map == 0 && map_fill == 0) return 0;
+    hipStream_t hs = static_cast<hipStream_t>(stream);
+
+    const size_t copy_bytes = kvp::align256((size_t)n_copies * sizeof(KvpRowCopy));
+    const size_t map_bytes = kvp::align256((size_t)n_map * sizeof(long));
+    const size_t need = copy_bytes + 2 * map_bytes;
+    KvpRowCopy* d_copies = nullptr;
+    long* d_rows = nullptr;
+    long* d_slots = nullptr;
+    if (need > 0) {
+        if (!st->reserve(need)) {
+            set_error("stage: descriptor ring allocation failed");
+            return 1;
+        }
+        unsigned char* h = st->host + st->head;
+        unsigned char* d = st->dev + st->head;
+        if (n_copies > 0) memcpy(h, copies, (size_t)n_copies * sizeof(KvpRowCopy));
+        if (n_map > 0) {
+            memcpy(h + copy_bytes, map_rows, (size_t)n_map * sizeof(long));
+            memcpy(h + copy_bytes + map_bytes, map_slots, (size_t)n_map * sizeof(long));
+        }
+        hipError_t e = hipMemcpyAsync(d, h, need, hipMemcpyHostToDevice, hs);
+        if (e != hipSuccess) {
+            set_error("stage: descriptor upload: %s", hipGetErrorString(e));
+            return 1;
+        }
+        d_copies = reinterpret_cast<KvpRowCopy*>(d);
+        d_rows = reinterpret_cast<long*>(d + copy_bytes);
+        d_slots = reinterpret_cast<long*>(d + copy_bytes + map_bytes);
+    }
+    if (map_fill > 0) {
+        long blocks = (map_fill + kvp::kMapThreads - 1) / kvp::kMapThreads;
+        if (blocks > 1024) blocks = 1024;
+        hipLaunchKernelGGL(kvp::map_fill_kernel, dim3((unsigned)blocks), dim3(kvp::kMapThreads), 0, hs,
+                           map_dev, map_fill);
+    }
+    const long map_blocks = (n_map + kvp::kStageThreads - 1) / kvp::kStageThreads;
+    const long blocks = n_copies + map_blocks;
+    if (blocks > 0) {
+        hipLaunchKernelGGL(kvp::stage_kernel, dim3((unsigned)blocks), dim3(kvp::kStageThreads), 0, hs,
+                           d_copies, n_copies, static_cast<unsigned char*>(arena), row_stride_bytes,
+                           d_rows, d_slots, n_map, map_dev);
+    }
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) {
+        set_error("stage launch: %s", hipGetErrorString(e));
+        return 1;
+    }
+    if (need > 0) {
+        hipEvent_t ev = st->take_event();
+        if (!ev || hipEventRecord(ev, hs) != hipSuccess) {
+            // Without a fence the region cannot be reused safely: drain now.
+            if (ev) st->spare.push_back(ev);
+            (void)hipStreamSynchronize(hs);
+        } else {
+            st->inflight.push_back(ev);
+        }
+        st->head += need;
+    }
+    return 0;
+}
+
+}  // extern "C"

@@ -1,0 +1,340 @@
+// Frame pipeline: the reference driver's per-frame loop
+// (reference: src/run_policy_experiment.cu:136-283) as a reusable library
+// object behind kvp_pipeline_*.
+//
+// Per frame f (policies other than "none"):
+//   1. policy select over the frame's tiles (intra) or the frame-major
+//      candidate prefix (cross), or only the window's frames when a sliding
+//      window is set;
+//   2. streaming: release the rows of tiles that dropped out of the
+//      selection, before staging (gid ascending, rows ascending);
+//   3. arena_begin_step, KVMap prefix [0, (f+1)*T) reset to -1, then every
+//      selected tile's rows staged in policy order, rows ascending, the map
+//      entry of each staged row set to its arena row / slot;
+//   4. one flush: device map rebuild + one gather launch for all copies;
+//   5. one attention launch for the frame.
+// Nothing synchronises the host per frame: staging, map rebuild and
+// attention are ordered on the pipeline's stream. The host map is kept for
+// introspection and plan-only use.
+
+#include <algorithm>
+#include <cstring>
+#include <memory>
+#include <new>
+#include <string>
+#include <vector>
+
+#include "kv_tile_manager.h"
+#include "kvp_c_api.h"
+#include "kvp_internal.h"
+#include "tile_gating_policy.h"
+
+namespace {
+
+struct Pipeline {
+    std::unique_ptr<TileGatingPolicy> policy;
+    bool persist = false;
+    bool cross = false;
+    bool streaming = false;
+    bool plan_only = false;
+    int frames = 0, T = 0, D = 0, heads = 0, tile_tokens = 0, window = 0, dtype = 0;
+    int elem = 4;
+    long num_tiles = 0;
+    long slots = 0;
+    long set_aside = 0;
+    std::unique_ptr<KVTileManager> mgr;
+    std::vector<long> h_map;
+    long* d_map = nullptr;
+    std::vector<long> ids;
+    int count = 0;
+    std::vector<char> selected, prev_selected;
+    std::vector<long> map_rows, map_slots;
+    long staged_tiles = 0;
+    long copy_rows = 0;
+    int next_frame = 0;
+    void* stream = nullptr;
+
+    ~Pipeline() {
+        mgr.reset();
+        if (d_map) {
+            kvp_stream_sync(stream);
+            kvp_dev_free(d_map);
+        }
+    }
+};
+
+Pipeline* PL(void* p) { return static_cast<Pipeline*>(p); }
+
+int step_frame(Pipeline& p, int f, const char* q, const char* k, const char* v, char* out,
+               const float* scores_flat) {
+    if (f != p.next_frame) {
+        kvp::set_error("pipeline: frame %d stepped out of order (expected %d)", f, p.next_frame);
+        return 1;
+    }
+    const long T = p.T;
+    const long D = p.D;
+    const long row_bytes = D * p.elem;
+    const long frame_bytes = T * row_bytes;
+    const bool need_data = !p.plan_only;
+    if (need_data && (!q || !k || !v || !out)) {
+        kvp::set_error("pipeline: null q/k/v/out");
+        return 1;
+    }
+
+    long kb_frame = 0;
+    if (p.cross && p.window > 0 && f + 1 > p.window) kb_frame = f + 1 - p.window;
+
+    if (!p.persist) {
+        p.count = 0;
+        p.staged_tiles = 0;
+        p.copy_rows = 0;
+        p.next_frame = (f + 1 == p.frames) ? 0 : f + 1;
+        if (p.plan_only) return 0;
+        // Same per-frame launch structure as the gated policies.
+        if (p.cross)
+            return kvp::launch_attention(p.dtype, q + f * frame_bytes, k, v, nullptr, nullptr,
+                                         out + f * frame_bytes, p.T, p.D, p.heads, 1, 0, 0, 0,
+                                         kb_frame * T, (long)(f + 1) * T, p.stream);
+        return kvp::launch_attention(p.dtype, q + f * frame_bytes, k + f * frame_bytes,
+                                     v + f * frame_bytes, nullptr, nullptr,
+                                     out + f * frame_bytes, p.T, p.D, p.heads, 1, 0, 0, 0, 0, T,
+                                     p.stream);
+    }
+    if (!scores_flat) {
+        kvp::set_error("pipeline: policy %s needs motion scores", p.policy->name());
+        return 1;
+    }
+
+    KVTileManager& mgr = *p.mgr;
+    if (f == 0) {
+        p.prev_selected.clear();
+        if (p.streaming && !mgr.streaming_begin()) {
+            kvp::set_error("pipeline: streaming_begin failed");
+            return 1;
+        }
+    }
+
+    // 1. selection
+    p.count = 0;
+    if (p.cross) {
+        const long first = kb_frame * p.num_tiles;
+        const long n = (long)(f + 1) * p.num_tiles - first;
+        p.policy->select_range(scores_flat, first, (int)n, (int)p.slots, p.ids.data(), &p.count);
+    } else {
+        p.policy->select(scores_flat + (long)f * p.num_tiles, (int)p.num_tiles, (int)p.slots,
+                         p.ids.data(), &p.count);
+    }
+
+    // 2. streaming release of tiles that dropped out
+    p.selected.assign((size_t)((f + 1) * p.num_tiles), 0);
+    for (int i = 0; i < p.count; ++i) {
+        const long id = p.ids[i];
+        if (id >= 0 && id < (long)p.selected.size()) p.selected[(size_t)id] = 1;
+    }
+    if (p.streaming && f > 0) {
+        const long prev_len = (long)p.prev_selected.size();
+        for (long gid = 0; gid < prev_len; ++gid) {
+            if (!p.prev_selected[(size_t)gid]) continue;
+            if (gid < (long)p.selected.size() && p.selected[(size_t)gid]) continue;
+            // Intra mode releases rows of the CURRENT frame, as the
+            // reference driver does (src/run_policy_experiment.cu:180-185).
+            const long src_f = p.cross ? gid / p.num_tiles : f;
+            const long tile = p.cross ? gid % p.num_tiles : gid;
+            const long t0 = tile * p.tile_tokens;
+            const long c = std::min((long)p.tile_tokens, T - t0);
+            for (long r = 0; r < c; ++r) mgr.streaming_release(src_f * T + t0 + r);
+        }
+    }
+
+    // 3. staging + host map
+    mgr.arena_begin_step();
+    std::fill(p.h_map.begin(), p.h_map.begin() + (size_t)(f + 1) * T, -1L);
+    p.map_rows.clear();
+    p.map_slots.clear();
+    p.staged_tiles = 0;
+    p.copy_rows = 0;
+    for (int i = 0; i < p.count; ++i) {
+        const long gid = p.ids[i];
+        const long src_f = p.cross ? gid / p.num_tiles : f;
+        const long tile = p.cross ? gid % p.num_tiles : gid;
+        const long t0 = tile * p.tile_tokens;
+        const long c = std::min((long)p.tile_tokens, T - t0);
+        bool all = true;
+        for (long r = 0; r < c && all; ++r) {
+            const long row_id = src_f * T + t0 + r;
+            const char* kp = k ? k + row_id * row_bytes : nullptr;
+            const char* vp = v ? v + row_id * row_bytes : nullptr;
+            long slot = -1;
+            if (p.streaming) {
+                bool restaged = false;
+                all = mgr.streaming_stage(row_id, kp, (size_t)row_bytes, vp, (size_t)row_bytes,
+                                          false, &slot, &restaged);
+                if (all && restaged) ++p.copy_rows;
+            } else {
+                all = mgr.arena_stage(kp, (size_t)row_bytes, vp, (size_t)row_bytes, &slot);
+                if (all) ++p.copy_rows;
+            }
+            if (all) {
+                p.h_map[(size_t)row_id] = slot;
+                p.map_rows.push_back(row_id);
+                p.map_slots.push_back(slot);
+            }
+        }
+        if (all) ++p.staged_tiles;
+    }
+
+    // 4. one flush: map rebuild + gather
+    if (!p.plan_only) {
+        if (!mgr.flush_with_map(p.d_map, (long)(f + 1) * T, p.map_rows.data(),
+                                p.map_slots.data(), p.map_rows.size())) {
+            return 1;
+        }
+    }
+    if (p.streaming)
+        (void)mgr.streaming_apply_window();
+    else
+        (void)mgr.arena_apply_window();
+
+    // 5. attention
+    int rc = 0;
+    if (!p.plan_only) {
+        const void* arena = mgr.arena_device_ptr();
+        if (p.cross)
+            rc = kvp::launch_attention(p.dtype, q + f * frame_bytes, k, v, arena, p.d_map,
+                                       out + f * frame_bytes, p.T, p.D, p.heads, 1, 0, 0, 0,
+                                       kb_frame * T, (long)(f + 1) * T, p.stream);
+        else
+            rc = kvp::launch_attention(p.dtype, q + f * frame_bytes, k + f * frame_bytes,
+                                       v + f * frame_bytes, arena, p.d_map + (long)f * T,
+                                       out + f * frame_bytes, p.T, p.D, p.heads, 1, 0, 0, 0, 0,
+                                       T, p.stream);
+    }
+
+    if (p.streaming)
+        p.prev_selected = p.selected;
+    else
+        mgr.arena_end_step();
+    if (p.streaming && f + 1 == p.frames) mgr.streaming_end();
+    p.next_frame = (f + 1 == p.frames) ? 0 : f + 1;
+    return rc;
+}
+
+}  // namespace
+
+extern "C" {
+
+void* kvp_pipeline_create(const char* policy, int cross, int streaming, int frames, int T,
+                          int D, int heads, int tile_tokens, long set_aside_bytes, int dtype,
+                          int window_frames, int plan_only) {
+    if (!policy || frames <= 0 || T <= 0 || heads <= 0 || D != heads * 128 ||
+        tile_tokens <= 0 || (dtype != 0 && dtype != 1) || window_frames < 0) {
+        kvp::set_error("pipeline: bad arguments");
+        return nullptr;
+    }
+    std::unique_ptr<Pipeline> p(new (std::nothrow) Pipeline());
+    if (!p) return nullptr;
+    p->num_tiles = (T + tile_tokens - 1) / tile_tokens;
+    p->policy.reset(make_tile_gating_policy(policy, (int)p->num_tiles, frames));
+    if (!p->policy) {
+        kvp::set_error("pipeline: unknown policy %s", policy);
+        return nullptr;
+    }
+    p->persist = strcmp(policy, "none") != 0;
+    p->cross = cross != 0;
+    p->streaming = streaming != 0 && p->persist;
+    p->plan_only = plan_only != 0;
+    p->frames = frames;
+    p->T = T;
+    p->D = D;
+    p->heads = heads;
+    p->tile_tokens = tile_tokens;
+    p->window = window_frames;
+    p->dtype = dtype;
+    p->elem = dtype == 1 ? 2 : 4;
+    p->set_aside = set_aside_bytes;
+    // slots = set_aside / (tile_tokens * hidden * elem * 2)
+    // (reference: src/run_policy_experiment.cu:143-144, fp32 there).
+    const long tile_bytes = (long)tile_tokens * D * p->elem * 2;
+    p->slots = set_aside_bytes > 0 ? set_aside_bytes / tile_bytes : 0;
+    p->ids.assign((size_t)std::max<long>((long)frames * p->num_tiles, p->slots) + 1, 0);
+    if (p->persist) {
+        if (set_aside_bytes <= 0) {
+            kvp::set_error("pipeline: policy %s needs a positive set-aside", policy);
+            return nullptr;
+        }
+        p->mgr.reset(new KVTileManager((size_t)set_aside_bytes, (size_t)set_aside_bytes));
+        const size_t stride_floats = (size_t)D * 2 * p->elem / sizeof(float);
+        const bool ok = p->mgr->init() &&
+                        (p->plan_only
+                             ? p->mgr->arena_attach(nullptr, (size_t)set_aside_bytes, stride_floats)
+                             : p->mgr->arena_init((size_t)set_aside_bytes, stride_floats));
+        if (!ok) {
+            kvp::set_error("pipeline: manager init failed");
+            return nullptr;
+        }
+        p->h_map.assign((size_t)frames * T, -1L);
+        if (!p->plan_only) {
+            p->d_map = static_cast<long*>(kvp_dev_alloc((size_t)frames * T * sizeof(long)));
+            if (!p->d_map) return nullptr;
+        }
+    }
+    return p.release();
+}
+
+void kvp_pipeline_destroy(void* p) { delete PL(p); }
+
+int kvp_pipeline_set_stream(void* p, void* stream) {
+    PL(p)->stream = stream;
+    if (PL(p)->mgr) PL(p)->mgr->set_stream(stream);
+    return 0;
+}
+
+int kvp_pipeline_step(void* p, int f, const void* q, const void* k, const void* v, void* out,
+                      const float* scores_flat) {
+    Pipeline& pl = *PL(p);
+    if (f < 0 || f >= pl.frames) {
+        kvp::set_error("pipeline: frame %d out of range", f);
+        return 1;
+    }
+    return step_frame(pl, f, static_cast<const char*>(q), static_cast<const char*>(k),
+                      static_cast<const char*>(v), static_cast<char*>(out), scores_flat);
+}
+
+int kvp_pipeline_run(void* p, const void* q, const void* k, const void* v, void* out,
+                     const float* scores_flat) {
+    Pipeline& pl = *PL(p);
+    pl.next_frame = 0;
+    for (int f = 0; f < pl.frames; ++f) {
+        const int rc = kvp_pipeline_step(p, f, q, k, v, out, scores_flat);
+        if (rc) return rc;
+    }
+    return 0;
+}
+
+int kvp_pipeline_selected(void* p, long* ids, int cap) {
+    Pipeline& pl = *PL(p);
+    const int n = std::min(pl.count, cap);
+    for (int i = 0; i < n; ++i) ids[i] = pl.ids[i];
+    return pl.count;
+}
+
+long kvp_pipeline_map(void* p, long* out, long cap) {
+    Pipeline& pl = *PL(p);
+    const long n = std::min((long)pl.h_map.size(), cap);
+    if (n > 0) memcpy(out, pl.h_map.data(), (size_t)n * sizeof(long));
+    return (long)pl.h_map.size();
+}
+
+long kvp_pipeline_slots(void* p) { return PL(p)->slots; }
+long kvp_pipeline_staged_tiles(void* p) { return PL(p)->staged_tiles; }
+long kvp_pipeline_staged_bytes(void* p) {
+    return PL(p)->mgr ? (long)PL(p)->mgr->streaming_staged_bytes() : 0;
+}
+long kvp_pipeline_copy_rows(void* p) { return PL(p)->copy_rows; }
+void* kvp_pipeline_arena(void* p) {
+    return PL(p)->mgr ? PL(p)->mgr->arena_device_ptr() : nullptr;
+}
+const long* kvp_pipeline_device_map(void* p) { return PL(p)->d_map; }
+void* kvp_pipeline_manager(void* p) { return PL(p)->mgr.get(); }
+
+}  // extern "C"

@@ -1,0 +1,184 @@
+"""GPU parity of the attention kernels against the CPU oracle.
+
+Tolerances: fp32 max-abs <= 1e-3 and mean-abs <= 1e-4
+against the fp32 golden (reference: tests/test_correctness.py:26-27);
+bf16 max-abs <= 2e-2 against the fp32 golden of bf16-rounded inputs.
+KVMap indirection must not change a single bit of the output.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from kvpersist import api, workloads
+from oracle import attention as at
+from oracle import trace_synth as ts
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+FP32_MAX, FP32_MEAN, BF16_MAX = 1e-3, 1e-4, 2e-2
+
+
+def _inputs(frames, T, heads, seed, dtype):
+    rng = np.random.default_rng(seed)
+    D = heads * 128
+    q, k, v = (torch.from_numpy(rng.standard_normal((frames * T, D), dtype=np.float32))
+               for _ in range(3))
+    if dtype == torch.bfloat16:
+        q, k, v = at.round_bf16(q), at.round_bf16(k), at.round_bf16(v)
+    return q, k, v
+
+
+def _run(dtype, q, k, v, frames, T, heads, mode, window=0, arena=None, kvmap=None):
+    """Per-frame launches through the C-ABI (intra: pre-offset; cross: full bases)."""
+    D = heads * 128
+    qd, kd, vd = (x.to(DEV).to(dtype).contiguous() for x in (q, k, v))
+    out = torch.empty_like(qd)
+    for f in range(frames):
+        sl = slice(f * T, (f + 1) * T)
+        if mode == "intra":
+            kv_k, kv_v = kd[sl], vd[sl]
+            mp = kvmap[sl] if kvmap is not None else None
+        else:
+            kv_k, kv_v, mp = kd, vd, kvmap
+        if dtype == torch.float32:
+            api.attn_forward_single_frame(qd[sl], kv_k, kv_v, arena, mp, out[sl], T, D, heads,
+                                          0 if mode == "intra" else 1, f, window)
+        else:
+            api.attn_forward_single_frame_bf16(qd[sl], kv_k, kv_v, arena, mp, out[sl], T, D,
+                                               heads, 0 if mode == "intra" else 1, f, window)
+    torch.cuda.synchronize()
+    return out.float().cpu()
+
+
+def _check(got, want, dtype):
+    err = (got - want).abs()
+    if dtype == torch.float32:
+        assert float(err.max()) <= FP32_MAX, float(err.max())
+        assert float(err.mean()) <= FP32_MEAN, float(err.mean())
+    else:
+        assert float(err.max()) <= BF16_MAX, float(err.max())
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("mode,window", [("intra", 0), ("cross", 0), ("cross", 2)])
+@pytest.mark.parametrize("T,heads", [(200, 2), (33, 1), (1, 1), (129, 3)])
+def test_small_shapes_match_oracle(dtype, mode, window, T, heads):
+    frames = 4
+    q, k, v = _inputs(frames, T, heads, seed=T * 7 + heads, dtype=dtype)
+    got = _run(dtype, q, k, v, frames, T, heads, mode, window)
+    want = at.attention_frames(q, k, v, frames, T, heads, mode, window)
+    _check(got, want, dtype)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_single_key_returns_value_row_exactly(dtype):
+    q, k, v = _inputs(1, 1, 2, seed=3, dtype=dtype)
+    got = _run(dtype, q, k, v, 1, 1, 2, "intra")
+    assert torch.equal(got, v.to(dtype).float())
+
+
+def _random_arena(k, v, rng, frac=0.3):
+    """Copy a random subset of K|V rows to permuted arena rows; return arena, map."""
+    rows = k.shape[0]
+    D = k.shape[1]
+    chosen = rng.choice(rows, size=max(1, int(frac * rows)), replace=False)
+    slots = rng.permutation(len(chosen))
+    arena = torch.zeros(len(chosen) + 3, 2 * D, dtype=k.dtype)
+    kvmap = torch.full((rows,), -1, dtype=torch.int64)
+    for r, s in zip(chosen, slots):
+        arena[s, :D] = k[r]
+        arena[s, D:] = v[r]
+        kvmap[r] = int(s)
+    return arena, kvmap
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("mode", ["intra", "cross"])
+def test_kvmap_indirection_is_bitwise_invisible(dtype, mode):
+    frames, T, heads = 3, 300, 2
+    q, k, v = _inputs(frames, T, heads, seed=11, dtype=dtype)
+    base = _run(dtype, q, k, v, frames, T, heads, mode)
+    rng = np.random.default_rng(12)
+    arena, kvmap = _random_arena(k.to(dtype), v.to(dtype), rng)
+    got = _run(dtype, q, k, v, frames, T, heads, mode, arena=arena.to(DEV).contiguous(),
+               kvmap=kvmap.to(DEV))
+    assert torch.equal(got, base)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_c1_full_frame(dtype):
+    """C1 shape: 1560 tokens x 12 heads x 128, policy none."""
+    T, heads = 1560, 12
+    q, k, v = (torch.from_numpy(x) for x in workloads.qkv_host(1, T, seed=42))
+    if dtype == torch.bfloat16:
+        q, k, v = at.round_bf16(q), at.round_bf16(k), at.round_bf16(v)
+    got = _run(dtype, q, k, v, 1, T, heads, "intra")
+    _check(got, at.attention_keys(q, k, v, heads), dtype)
+
+
+def test_reference_trace_baseline_launcher():
+    """The reference correctness scoreboard: baseline launcher (remap=false,
+    8 frames in one launch) on the reference's own seed-42 trace against the
+    fp32 golden, max-abs < 1e-3 and mean-abs < 1e-4 per frame
+    (reference: tests/test_correctness.py:26-27,86-97)."""
+    torch.set_num_threads(min(16, max(1, torch.get_num_threads())))
+    tr = ts.synthetic_trace(frames=8, seed=42)
+    T, D, heads = 1560, 1536, 12
+    q = tr["q"].reshape(-1, D).to(DEV)
+    k = tr["k"].reshape(-1, D).to(DEV)
+    v = tr["v"].reshape(-1, D).to(DEV)
+    out = torch.empty_like(q)
+    api.attn_forward_launcher(q, k, v, None, None, out, 8, T, D, heads, remap=False)
+    torch.cuda.synchronize()
+    got = out.cpu().view(8, T, D)
+    for f in range(8):
+        want = at.attention_keys(tr["q"][f], tr["k"][f], tr["v"][f], heads)
+        err = (got[f] - want).abs()
+        assert float(err.max()) < FP32_MAX and float(err.mean()) < FP32_MEAN, f
+
+
+def test_launcher_remap_equals_baseline():
+    frames, T, heads = 3, 257, 2
+    q, k, v = _inputs(frames, T, heads, seed=21, dtype=torch.float32)
+    D = heads * 128
+    rng = np.random.default_rng(22)
+    arena, kvmap_abs = _random_arena(k, v, rng, frac=0.4)
+    # remap=true slices the map per frame: map[f*T + j] for key j of frame f
+    qd, kd, vd = q.to(DEV), k.to(DEV), v.to(DEV)
+    out_a = torch.empty_like(qd)
+    out_b = torch.empty_like(qd)
+    api.attn_forward_launcher(qd, kd, vd, None, None, out_a, frames, T, D, heads, remap=False)
+    api.attn_forward_launcher(qd, kd, vd, arena.to(DEV), kvmap_abs.to(DEV), out_b, frames, T, D,
+                              heads, remap=True)
+    torch.cuda.synchronize()
+    assert torch.equal(out_a.cpu(), out_b.cpu())
+    want = at.attention_frames(q, k, v, frames, T, heads, "intra")
+    _check(out_a.cpu(), want, torch.float32)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_split_and_unsplit_launches(dtype):
+    """One frame of 1560 queries splits the key range (grid underfill); eight
+    frames in one launch do not. Both paths must match the oracle."""
+    T, heads = 1560, 12
+    d = 1 if dtype == torch.bfloat16 else 0
+    assert api.attn_splits(d, T, heads, 1, T) > 1
+    assert api.attn_splits(d, T, heads, 8, T) == 1
+    q, k, v = _inputs(2, T, heads, seed=31, dtype=dtype)
+    got = _run(dtype, q, k, v, 2, T, heads, "cross")
+    want = at.attention_frames(q, k, v, 2, T, heads, "cross")
+    _check(got, want, dtype)
+
+
+def test_bad_arguments_are_rejected_before_launch(lib):
+    x = torch.zeros(64, 256, device=DEV)
+    # map without arena
+    m = torch.zeros(64, dtype=torch.int64, device=DEV)
+    rc = lib.kvp_attn_forward_range(0, x.data_ptr(), x.data_ptr(), x.data_ptr(), None,
+                                    m.data_ptr(), x.data_ptr(), 64, 256, 2, 0, 64, None)
+    assert rc != 0
+    # misaligned pointer
+    rc = lib.kvp_attn_forward_range(0, x.data_ptr() + 4, x.data_ptr(), x.data_ptr(), None, None,
+                                    x.data_ptr(), 63, 256, 2, 0, 63, None)
+    assert rc != 0

@@ -1,0 +1,164 @@
+"""GPU parity of the full frame pipeline (select -> stage -> map -> attention).
+
+Gates, as the reference harness has them (reference:
+tests/test_policy_variants.py:174-179,228-230):
+  * outputs bitwise equal across policies within a configuration;
+  * streaming (sticky slots) outputs bitwise equal to dense arena outputs;
+  * outputs within tolerance of the CPU golden.
+Plus the invariants the arena must satisfy on the device:
+  * the device KVMap equals the oracle driver's map, bit for bit;
+  * every mapped row's arena slot holds exactly [K row | V row] (bitwise),
+    i.e. the arena layout matches the reference manager's.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from kvpersist import FramePipeline, workloads
+from oracle import attention as at
+from oracle import manager as mm
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+D, HEADS = workloads.HIDDEN, workloads.HEADS
+
+
+def _device_inputs(frames, T, dtype, seed):
+    q, k, v = (torch.from_numpy(x) for x in workloads.qkv_host(frames, T, seed=seed))
+    if dtype == torch.bfloat16:
+        q, k, v = at.round_bf16(q), at.round_bf16(k), at.round_bf16(v)
+    return q, k, v, q.to(DEV).to(dtype), k.to(DEV).to(dtype), v.to(DEV).to(dtype)
+
+
+def _arena_rows(pl, nrows, dtype):
+    n = nrows * 2 * D
+    buf = torch.empty(n, dtype=dtype, device=DEV)
+    esz = 4 if dtype == torch.float32 else 2
+    torch.cuda.synchronize()
+    from kvpersist import _lib
+    lib = _lib.load()
+    assert lib.kvp_memcpy_d2d(buf.data_ptr(), pl.arena_ptr(), n * esz, None) == 0
+    torch.cuda.synchronize()
+    return buf.view(nrows, 2 * D)
+
+
+def _device_map(pl, n):
+    from kvpersist import _lib
+    lib = _lib.load()
+    host = np.empty(n, dtype=np.int64)
+    torch.cuda.synchronize()
+    assert lib.kvp_memcpy_d2h(host.ctypes.data, pl.device_map_ptr(), n * 8, None) == 0
+    return host
+
+
+def _run_pipeline(policy, *, cross, streaming, frames, T, dtype, set_aside, scores, qkv,
+                  window=0, check_arena=False):
+    _, _, _, qd, kd, vd = qkv
+    out = torch.empty_like(qd)
+    d = 0 if dtype == torch.float32 else 1
+    elem = 4 if dtype == torch.float32 else 2
+    pl = FramePipeline(policy, cross=cross, streaming=streaming, frames=frames, T=T, D=D,
+                       heads=HEADS, tile_tokens=16, set_aside_bytes=set_aside, dtype=d,
+                       window_frames=window)
+    pl.set_scores(scores)
+    plan = None
+    if check_arena and policy != "none":
+        plan = mm.plan_frames(policy, cross=cross, streaming=streaming, frames=frames, T=T, D=D,
+                              tile_tokens=16, set_aside=set_aside, elem=elem,
+                              scores_flat=scores, window_frames=window)
+    kflat, vflat = kd.view(frames * T, D), vd.view(frames * T, D)
+    for f in range(frames):
+        pl.step(f, qd, kd, vd, out)
+        if plan is not None:
+            dmap = _device_map(pl, (f + 1) * T)
+            np.testing.assert_array_equal(dmap, plan[f]["map"], err_msg=f"map frame {f}")
+            rows = np.nonzero(dmap >= 0)[0]
+            if rows.size:
+                cap = set_aside // (2 * D * elem)
+                arena = _arena_rows(pl, cap, dtype)
+                slots = torch.from_numpy(dmap[rows]).to(DEV)
+                ridx = torch.from_numpy(rows).to(DEV)
+                assert torch.equal(arena[slots, :D], kflat[ridx]), f
+                assert torch.equal(arena[slots, D:], vflat[ridx]), f
+    torch.cuda.synchronize()
+    pl.close()
+    return out
+
+
+def test_c2_motion_arena_bit_exact_and_bitwise_output():
+    cfg = workloads.CONFIGS["c2"]
+    T = cfg.tokens
+    qkv = _device_inputs(1, T, torch.float32, seed=42)
+    scores = workloads.motion_for(cfg)
+    base = _run_pipeline("none", cross=False, streaming=False, frames=1, T=T,
+                         dtype=torch.float32, set_aside=0, scores=None, qkv=qkv)
+    got = _run_pipeline("motion", cross=False, streaming=False, frames=1, T=T,
+                        dtype=torch.float32, set_aside=cfg.set_aside, scores=scores, qkv=qkv,
+                        check_arena=True)
+    assert torch.equal(got, base)
+    want = at.attention_keys(qkv[0], qkv[1], qkv[2], HEADS)
+    err = (got.cpu() - want).abs()
+    assert float(err.max()) <= 1e-3 and float(err.mean()) <= 1e-4
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_cross_policies_bitwise_and_streaming_equals_dense(dtype):
+    cfg = workloads.CONFIGS["c3"]
+    frames, T = 4, cfg.tokens
+    qkv = _device_inputs(frames, T, dtype, seed=5)
+    scores = workloads.motion_for(cfg, 0)[:frames]
+    set_aside = cfg.set_aside if dtype == torch.bfloat16 else 2 * cfg.set_aside
+    base = _run_pipeline("none", cross=True, streaming=False, frames=frames, T=T, dtype=dtype,
+                         set_aside=0, scores=None, qkv=qkv)
+    for streaming in (False, True):
+        for policy in ("uniform", "recency", "motion", "reuse_weighted"):
+            got = _run_pipeline(policy, cross=True, streaming=streaming, frames=frames, T=T,
+                                dtype=dtype, set_aside=set_aside, scores=scores, qkv=qkv,
+                                check_arena=(policy == "motion"))
+            assert torch.equal(got, base), (policy, streaming)
+    # golden: frames 0 and 1 in full, the last frame on its first 256 queries
+    q, k, v = qkv[0], qkv[1], qkv[2]
+    tol = 1e-3 if dtype == torch.float32 else 2e-2
+    outc = base.float().cpu()
+    for f in (0, 1):
+        want = at.attention_keys(q[f * T:(f + 1) * T], k[:(f + 1) * T], v[:(f + 1) * T], HEADS)
+        assert float((outc[f * T:(f + 1) * T] - want).abs().max()) <= tol, f
+    f = frames - 1
+    want = at.attention_keys(q[f * T:f * T + 256], k[:(f + 1) * T], v[:(f + 1) * T], HEADS)
+    assert float((outc[f * T:f * T + 256] - want).abs().max()) <= tol
+
+
+def test_sliding_window_pipeline_bf16():
+    cfg = workloads.CONFIGS["c4"]
+    frames, T, W = 11, cfg.tokens, cfg.window
+    qkv = _device_inputs(frames, T, torch.bfloat16, seed=8)
+    scores = workloads.motion_for(cfg, 0)[:frames]
+    base = _run_pipeline("none", cross=True, streaming=False, frames=frames, T=T,
+                         dtype=torch.bfloat16, set_aside=0, scores=None, qkv=qkv, window=W)
+    for policy in ("recency", "motion", "reuse_weighted"):
+        got = _run_pipeline(policy, cross=True, streaming=True, frames=frames, T=T,
+                            dtype=torch.bfloat16, set_aside=cfg.set_aside, scores=scores,
+                            qkv=qkv, window=W, check_arena=(policy == "reuse_weighted"))
+        assert torch.equal(got, base), policy
+    q, k, v = qkv[0], qkv[1], qkv[2]
+    f = frames - 1
+    b = (f + 1 - W) * T
+    want = at.attention_keys(q[f * T:f * T + 128], k[b:(f + 1) * T], v[b:(f + 1) * T], HEADS)
+    assert float((base.float().cpu()[f * T:f * T + 128] - want).abs().max()) <= 2e-2
+
+
+def test_c5_shape_single_frame_pair_bf16():
+    cfg = workloads.CONFIGS["c5"]
+    frames, T = 2, cfg.tokens
+    qkv = _device_inputs(frames, T, torch.bfloat16, seed=9)
+    scores = workloads.motion_for(cfg, 0)[:frames]
+    base = _run_pipeline("none", cross=True, streaming=False, frames=frames, T=T,
+                         dtype=torch.bfloat16, set_aside=0, scores=None, qkv=qkv)
+    got = _run_pipeline("motion", cross=True, streaming=True, frames=frames, T=T,
+                        dtype=torch.bfloat16, set_aside=cfg.set_aside, scores=scores, qkv=qkv,
+                        check_arena=True)
+    assert torch.equal(got, base)
+    q, k, v = qkv[0], qkv[1], qkv[2]
+    want = at.attention_keys(q[T:T + 128], k[:2 * T], v[:2 * T], HEADS)
+    assert float((base.float().cpu()[T:T + 128] - want).abs().max()) <= 2e-2
