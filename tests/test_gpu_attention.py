@@ -159,16 +159,18 @@ def test_launcher_remap_equals_baseline():
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 def test_split_and_unsplit_launches(dtype):
-    """One frame of 1560 queries splits the key range (grid underfill); eight
-    frames in one launch do not. Both paths must match the oracle."""
+    """One frame of 1560 queries splits the key range (grid underfill); a short
+    key range (fewer than 8 key tiles) never does. Both paths must match the
+    oracle."""
     T, heads = 1560, 12
     d = 1 if dtype == torch.bfloat16 else 0
     assert api.attn_splits(d, T, heads, 1, T) > 1
-    assert api.attn_splits(d, T, heads, 8, T) == 1
-    q, k, v = _inputs(2, T, heads, seed=31, dtype=dtype)
-    got = _run(dtype, q, k, v, 2, T, heads, "cross")
-    want = at.attention_frames(q, k, v, 2, T, heads, "cross")
-    _check(got, want, dtype)
+    assert api.attn_splits(d, 200, heads, 1, 200) == 1
+    for t, frames in ((T, 2), (200, 3)):
+        q, k, v = _inputs(frames, t, heads, seed=31, dtype=dtype)
+        got = _run(dtype, q, k, v, frames, t, heads, "cross")
+        want = at.attention_frames(q, k, v, frames, t, heads, "cross")
+        _check(got, want, dtype)
 
 
 def test_bad_arguments_are_rejected_before_launch(lib):
