@@ -204,16 +204,101 @@ __device__ __forceinline__ float softmax_update(float (&s)[N], float scale_log2,
 
 // ---------------------------------------------------------------------------
 // bf16 kernel
+//
+// K and V tiles (64 keys x 128 dims, 16 KiB each) stream global -> LDS with
+// global_load_lds_dwordx4 (no register staging) into a two-stage ring: the
+// loads of tile t+1 are in flight while tile t is computed. Lane l of the
+// wave's load instruction writes LDS bytes [base + 16*l, +16); it picks the
+// global 16-byte chunk that belongs at that (swizzled) LDS position.
+//
+// LDS layouts (row = key in tile, 256 B per row, 16 chunks of 16 B):
+//   K: physical chunk = logical chunk ^ (row & 15)
+//      (ds_read_b128 of 32 rows x one chunk is conflict free)
+//   V: physical chunk = logical chunk ^ kVSwz[row & 3], kVSwz = {0,6,12,10}
+//      (ds_read_b64_tr_b16 reads 4 consecutive rows x 32 B per 16-lane group;
+//       the table keeps those 4 x 32 B on distinct banks for 32- and 64-bank
+//       LDS models alike)
+// ds_read_b64_tr_b16: in each 16-lane group, source lane 4s+r addresses row s,
+// columns 4r..4r+3 of a 4 x 16 block; result lane j receives column j, rows
+// 0..3. That yields the V^T operand of O^T = V^T P^T directly.
+//
+// Softmax: scores stay in the log2 domain (scale folded into one FMA before
+// v_exp_f32). The running max used for exponentiation is only raised when a
+// lane's tile max exceeds it by more than kLazyRescale (2^8): O and l are then
+// rescaled together (wave-uniform branch). Until then p <= 2^8, exact in
+// fp32/bf16 range, and O/l is unchanged mathematically.
 // ---------------------------------------------------------------------------
 
-constexpr int kBf16KBytes = kBf16BlockKeys * kHeadDim * 2;  // 16 KiB
-constexpr int kBf16VBytes = kHeadDim * kBf16BlockKeys * 2;  // 16 KiB
+constexpr int kBf16TileBytes = kBf16BlockKeys * kHeadDim * 2;  // 16 KiB
+constexpr float kLazyRescale = 8.0f;
+constexpr unsigned kVSwzTable = 0xAC60u;  // nibbles {0, 6, 12, 10}
+
+typedef __attribute__((ext_vector_type(4))) short v4i16;
+typedef __attribute__((ext_vector_type(2))) __bf16 bf16x2;
+#define KVP_LDS __attribute__((address_space(3)))
+
+__device__ __forceinline__ unsigned vswz(int row) { return (kVSwzTable >> (4 * (row & 3))) & 15u; }
+
+// s_waitcnt immediates (gfx9 encoding): vmcnt in [3:0] and [15:14],
+// expcnt [6:4] = 7 and lgkmcnt [11:8] = 15 leave those counters alone.
+constexpr int waitcnt_vm(int n) { return (n & 15) | (7 << 4) | (15 << 8) | ((n >> 4) << 14); }
+
+__device__ __forceinline__ void swap_halves(float x, float& lo, float& hi) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false,
+                                                    false);
+    lo = __uint_as_float(r[0]);
+    hi = __uint_as_float(r[1]);
+}
+
+// LDS access of the compute phase is written as inline asm on purpose: the
+// K/V tiles arrive by asynchronous global->LDS copies (global_load_lds), and
+// the compiler, unable to prove that a read of the current stage does not
+// alias the copies in flight to the other stage, would otherwise wait for
+// every outstanding copy (vmcnt(0)) before each read. Completion is tracked
+// explicitly instead:
+//   * vmcnt: before the barrier that publishes a stage, each wave waits for
+//     its own copies of that stage (the next stage's copies stay in flight);
+//   * lgkmcnt: each batch of LDS reads is waited for by an asm statement that
+//     takes the destination registers as in/out operands, so no use of the
+//     data can be scheduled before the wait.
+// All these asm statements are volatile with a memory clobber, which keeps
+// them in program order relative to one another and to the barrier.
+
+__device__ __forceinline__ void wg_barrier() { asm volatile("s_barrier" ::: "memory"); }
+
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+template <int OFF>
+__device__ __forceinline__ u32x4 lds_b128(unsigned addr) {
+    u32x4 r;
+    asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(r) : "v"(addr), "n"(OFF) : "memory");
+    return r;
+}
+
+template <int OFF>
+__device__ __forceinline__ u32x2 lds_tr16(unsigned addr) {
+    u32x2 r;
+    asm volatile("ds_read_b64_tr_b16 %0, %1 offset:%2" : "=v"(r) : "v"(addr), "n"(OFF) : "memory");
+    return r;
+}
+
+__device__ __forceinline__ void lgkm_wait2(u32x4& a, u32x4& b) {
+    asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(a), "+v"(b)::"memory");
+}
+
+__device__ __forceinline__ void lgkm_wait_tr(u32x2& a, u32x2& b, u32x2& c, u32x2& d) {
+    asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(a), "+v"(b), "+v"(c), "+v"(d)::"memory");
+}
 
 template <typename OutT>
 __global__ __launch_bounds__(kThreads, 2) void attn_fwd_bf16_kernel(AttnArgs a) {
-    __shared__ __attribute__((aligned(16))) unsigned char lds[kBf16KBytes + kBf16VBytes];
-    unsigned char* ks_lds = lds;
-    unsigned char* vt_lds = lds + kBf16KBytes;
+    __shared__ __attribute__((aligned(1024))) unsigned char k_lds0[kBf16TileBytes];
+    __shared__ __attribute__((aligned(1024))) unsigned char v_lds0[kBf16TileBytes];
+    __shared__ __attribute__((aligned(1024))) unsigned char k_lds1[kBf16TileBytes];
+    __shared__ __attribute__((aligned(1024))) unsigned char v_lds1[kBf16TileBytes];
 
     const WgCoord c = decode_wg(a);
     const int tid = threadIdx.x;
@@ -225,75 +310,76 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_bf16_kernel(AttnArgs a) 
     const long kbeg = a.key_begin + (long)c.split * a.keys_per_split;
     long kend = kbeg + a.keys_per_split;
     if (kend > a.key_end) kend = a.key_end;
+    const int ntiles = (int)((kend - kbeg + kBf16BlockKeys - 1) / kBf16BlockKeys);
 
     const __bf16* Q = reinterpret_cast<const __bf16*>(a.q) + (long)c.frame * a.q_fstride;
-    const __bf16* K = reinterpret_cast<const __bf16*>(a.k) + (long)c.frame * a.kv_fstride;
-    const __bf16* V = reinterpret_cast<const __bf16*>(a.v) + (long)c.frame * a.kv_fstride;
-    const __bf16* A = reinterpret_cast<const __bf16*>(a.arena);
+    const unsigned char* Kb = reinterpret_cast<const unsigned char*>(a.k) + 2L * c.frame * a.kv_fstride;
+    const unsigned char* Vb = reinterpret_cast<const unsigned char*>(a.v) + 2L * c.frame * a.kv_fstride;
+    const unsigned char* Ab = reinterpret_cast<const unsigned char*>(a.arena);
     const long* map = a.kvmap ? a.kvmap + (long)c.frame * a.map_fstride : nullptr;
-    const int hoff = c.head * kHeadDim;
-    const long D = a.D;
+    const long row_bytes = 2L * a.D;
+    const long hoff_b = 2L * c.head * kHeadDim;
 
-    // Query fragment (B operand of S^T = K Q^T): lane holds
-    // Q[q][16*ks + 8*hh .. +8) for ks = 0..7.
+    // Query fragment (B operand of S^T = K Q^T): Q[q][16*ks + 8*hh .. +8).
     const int q = c.qb * kBlockQ + wave * 32 + lq;
     const int qc = q < a.nq ? q : a.nq - 1;
     bf16x8 qf[8];
     {
-        const __bf16* qp = Q + (long)qc * D + hoff + 8 * hh;
+        const __bf16* qp = Q + (long)qc * a.D + c.head * kHeadDim + 8 * hh;
 #pragma unroll
         for (int ks = 0; ks < 8; ++ks)
             qf[ks] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(qp + 16 * ks));
+        // Resolve the Q loads before the copy pipeline starts, so the loop
+        // never waits for vector memory on their account.
+        __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
     }
 
-    // Global->LDS staging assignment: 16-byte chunk ch of the head slice,
-    // keys 4*grp .. 4*grp+3 of the tile.
-    const int ld_ch = tid & 15;
-    const int ld_grp = tid >> 4;
+    // Load assignment: instruction i of wave w fills LDS bytes [(4w+i)*1 KiB, +1 KiB)
+    // of each tile: rows 16w + 4i + lane/16, physical chunk lane % 16.
+    const int ld_row0 = 16 * wave + (lane >> 4);
+    const int ld_pch = lane & 15;
 
-    u32x4 kr[4], vr[4];
-    auto load_tile = [&](long t0) {
+    // KVMap entries of a tile are fetched one tile ahead of its K/V loads so
+    // that their latency hides behind a tile of compute.
+    long mp[4] = {-1L, -1L, -1L, -1L};
+    auto load_map = [&](int t) {
+        if (!map) return;
+        const long t0 = kbeg + (long)t * kBf16BlockKeys;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            const long j = t0 + 4 * ld_grp + i;
-            if (j < kend) {
-                const long m = map ? map[j] : -1L;
-                const __bf16* kp = m >= 0 ? A + m * 2 * D + hoff : K + j * D + hoff;
-                const __bf16* vp = m >= 0 ? A + m * 2 * D + D + hoff : V + j * D + hoff;
-                kr[i] = *reinterpret_cast<const u32x4*>(kp + 8 * ld_ch);
-                vr[i] = *reinterpret_cast<const u32x4*>(vp + 8 * ld_ch);
-            } else {
-                kr[i] = u32x4{0u, 0u, 0u, 0u};
-                vr[i] = u32x4{0u, 0u, 0u, 0u};
-            }
+            long j = t0 + ld_row0 + 4 * i;
+            if (j >= kend) j = kend - 1;
+            mp[i] = map[j];
         }
     };
-    auto store_tile = [&]() {
-        // K: row-major [64][256 B], chunk swizzle ch ^ (row & 15).
+    auto issue_tile = [&](int t, unsigned char* kdst, unsigned char* vdst) {
+        const long t0 = kbeg + (long)t * kBf16BlockKeys;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            const int row = 4 * ld_grp + i;
-            *reinterpret_cast<u32x4*>(ks_lds + row * 256 + ((ld_ch ^ (row & 15)) << 4)) = kr[i];
+            const int row = ld_row0 + 4 * i;
+            long j = t0 + row;
+            if (j >= kend) j = kend - 1;  // clamped rows are masked out of the softmax
+            const long m = mp[i];
+            const unsigned char* kp = m >= 0 ? Ab + m * 2 * row_bytes : Kb + j * row_bytes;
+            const unsigned char* vp = m >= 0 ? Ab + m * 2 * row_bytes + row_bytes : Vb + j * row_bytes;
+            const unsigned kc = (unsigned)ld_pch ^ (unsigned)(row & 15);
+            const unsigned vc = (unsigned)ld_pch ^ vswz(row);
+            __builtin_amdgcn_global_load_lds(kp + hoff_b + 16 * kc,
+                                             (KVP_LDS void*)(kdst + (4 * wave + i) * 1024), 16, 0, 0);
+            __builtin_amdgcn_global_load_lds(vp + hoff_b + 16 * vc,
+                                             (KVP_LDS void*)(vdst + (4 * wave + i) * 1024), 16, 0, 0);
         }
-        // V: transposed [128 d][64 keys]. Within each group of 16 keys the
-        // position is 8*((k>>2)&1) + 4*(k>>3) + (k&3), so that lane half hh
-        // of the PV MFMA reads its 8 keys as one contiguous 16-byte chunk.
-        const int pos0 = 16 * (ld_grp >> 2) + 8 * (ld_grp & 1) + 4 * ((ld_grp >> 1) & 1);
-        const int vch = pos0 >> 3;
-        const int vsub = (pos0 & 7) << 1;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            const unsigned x0 = vr[0][e], x1 = vr[1][e], x2 = vr[2][e], x3 = vr[3][e];
-            u32x2 lo, hi;
-            lo[0] = (x0 & 0xffffu) | (x1 << 16);
-            lo[1] = (x2 & 0xffffu) | (x3 << 16);
-            hi[0] = (x0 >> 16) | (x1 & 0xffff0000u);
-            hi[1] = (x2 >> 16) | (x3 & 0xffff0000u);
-            const int d0 = 8 * ld_ch + 2 * e;
-            const int d1 = d0 + 1;
-            *reinterpret_cast<u32x2*>(vt_lds + d0 * 128 + ((vch ^ (d0 & 7)) << 4) + vsub) = lo;
-            *reinterpret_cast<u32x2*>(vt_lds + d1 * 128 + ((vch ^ (d1 & 7)) << 4) + vsub) = hi;
-        }
+    };
+    // Waits until the K/V loads of the tile about to be computed have landed:
+    // the next tile's 8 loads (and, with a map, 4 prefetched map loads) may
+    // still be in flight.
+    auto wait_current = [&](bool more) {
+        if (!more)
+            wait_vm<0>();
+        else if (map)
+            wait_vm<12>();
+        else
+            wait_vm<8>();
     };
 
     f32x16 o[4];
@@ -303,30 +389,45 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_bf16_kernel(AttnArgs a) 
         for (int v = 0; v < 16; ++v) o[nb][v] = 0.f;
     float m_run = -INFINITY;
     float l_run = 0.f;
+    const float cl2 = a.scale_log2;
 
-    long t0 = kbeg;
-    if (t0 < kend) load_tile(t0);
-    for (; t0 < kend; t0 += kBf16BlockKeys) {
-        store_tile();
-        __syncthreads();
-        if (t0 + kBf16BlockKeys < kend) load_tile(t0 + kBf16BlockKeys);
+    // Per-lane parts of the LDS read addresses.
+    const unsigned kswz = (unsigned)(lq & 15);
+    const int grp = lane >> 4;
+    const int tr_s = (lane & 15) >> 2;
+    const int tr_r = lane & 3;
+    const unsigned vs = vswz(tr_s);
+    const int vsub = 8 * (tr_r & 1);
+    const unsigned vcl = (unsigned)(2 * (grp & 1) + (tr_r >> 1));  // chunk bits below 4*nb
 
-        // S^T for two 32-key blocks.
+    auto compute_tile = [&](int t, const unsigned char* ks_lds, const unsigned char* vt_lds) {
+        const unsigned kbase = (unsigned)(uintptr_t)ks_lds + (unsigned)(lq * 256);
         f32x16 s0, s1;
 #pragma unroll
         for (int v = 0; v < 16; ++v) {
             s0[v] = 0.f;
             s1[v] = 0.f;
         }
+        // S^T = K Q^T, K fragments read two k-steps ahead of their MFMAs
+        u32x4 ka[2], kb[2];
+        {
+            const unsigned ad = kbase + ((((unsigned)hh) ^ kswz) << 4);
+            ka[0] = lds_b128<0>(ad);
+            kb[0] = lds_b128<32 * 256>(ad);
+        }
 #pragma unroll
         for (int ks = 0; ks < 8; ++ks) {
-            const int chs = ((2 * ks + hh) ^ (lq & 15)) << 4;
-            const bf16x8 ka = __builtin_bit_cast(
-                bf16x8, *reinterpret_cast<const u32x4*>(ks_lds + lq * 256 + chs));
-            const bf16x8 kb = __builtin_bit_cast(
-                bf16x8, *reinterpret_cast<const u32x4*>(ks_lds + (32 + lq) * 256 + chs));
-            s0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ka, qf[ks], s0, 0, 0, 0);
-            s1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kb, qf[ks], s1, 0, 0, 0);
+            const int cur = ks & 1;
+            lgkm_wait2(ka[cur], kb[cur]);
+            if (ks + 1 < 8) {
+                const unsigned ad = kbase + ((((unsigned)(2 * (ks + 1) + hh)) ^ kswz) << 4);
+                ka[cur ^ 1] = lds_b128<0>(ad);
+                kb[cur ^ 1] = lds_b128<32 * 256>(ad);
+            }
+            s0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, ka[cur]),
+                                                         qf[ks], s0, 0, 0, 0);
+            s1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, kb[cur]),
+                                                         qf[ks], s1, 0, 0, 0);
         }
 
         float s[32];
@@ -335,6 +436,7 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_bf16_kernel(AttnArgs a) 
             s[v] = s0[v];
             s[16 + v] = s1[v];
         }
+        const long t0 = kbeg + (long)t * kBf16BlockKeys;
         if (t0 + kBf16BlockKeys > kend) {
             const long lim = kend - t0;
 #pragma unroll
@@ -343,28 +445,91 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_bf16_kernel(AttnArgs a) 
                 if (key >= lim) s[v] = -INFINITY;
             }
         }
-        const float corr = softmax_update<32>(s, a.scale_log2, m_run, l_run);
+
+        // row max over this tile (both lane halves hold disjoint keys)
+        float mx = fmaxf(fmaxf(s[0], s[1]), s[2]);
+#pragma unroll
+        for (int v = 3; v < 31; v += 2) mx = fmaxf(fmaxf(mx, s[v]), s[v + 1]);
+        mx = fmaxf(mx, s[31]);
+        float mlo, mhi;
+        swap_halves(mx, mlo, mhi);
+        mx = fmaxf(mlo, mhi) * cl2;
+        if (__builtin_amdgcn_ballot_w64(mx > m_run + kLazyRescale)) {
+            const float m_new = fmaxf(m_run, mx);
+            const float corr = fast_exp2(m_run - m_new);
+            l_run *= corr;
+#pragma unroll
+            for (int nb = 0; nb < 4; ++nb)
+#pragma unroll
+                for (int v = 0; v < 16; ++v) o[nb][v] *= corr;
+            m_run = m_new;
+        }
 
         bf16x8 pb[4];
+        float rs = 0.f;
 #pragma unroll
-        for (int g = 0; g < 4; ++g)
+        for (int g = 0; g < 4; ++g) {
 #pragma unroll
-            for (int i = 0; i < 8; ++i) pb[g][i] = (__bf16)s[8 * g + i];
-
-#pragma unroll
-        for (int nb = 0; nb < 4; ++nb) {
-#pragma unroll
-            for (int v = 0; v < 16; ++v) o[nb][v] *= corr;
-            const int d = 32 * nb + lq;
-#pragma unroll
-            for (int g = 0; g < 4; ++g) {
-                const int ch = 2 * g + hh;
-                const bf16x8 va = __builtin_bit_cast(
-                    bf16x8, *reinterpret_cast<const u32x4*>(vt_lds + d * 128 + ((ch ^ (d & 7)) << 4)));
-                o[nb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(va, pb[g], o[nb], 0, 0, 0);
+            for (int i = 0; i < 8; i += 2) {
+                bf16x2 pr;
+                pr[0] = (__bf16)fast_exp2(fmaf(s[8 * g + i], cl2, -m_run));
+                pr[1] = (__bf16)fast_exp2(fmaf(s[8 * g + i + 1], cl2, -m_run));
+                pb[g][i] = pr[0];
+                pb[g][i + 1] = pr[1];
+                const bf16x2 one = {(__bf16)1.0f, (__bf16)1.0f};
+                rs = __builtin_amdgcn_fdot2_f32_bf16(pr, one, rs, false);
             }
         }
-        __syncthreads();
+        float rlo, rhi;
+        swap_halves(rs, rlo, rhi);
+        l_run += rlo + rhi;
+
+        // O^T += V^T P^T; transposed V reads of rows 16g + 4hh + s and +8
+        // (row offsets 16g*256 and 8*256 are immediates).
+        const unsigned vbase = (unsigned)(uintptr_t)vt_lds + (unsigned)((4 * hh + tr_s) * 256 + vsub);
+#pragma unroll
+        for (int nb = 0; nb < 4; ++nb) {
+            const unsigned ad = vbase + ((((unsigned)(4 * nb) | vcl) ^ vs) << 4);
+            u32x2 v0 = lds_tr16<0>(ad), v1 = lds_tr16<8 * 256>(ad);
+            u32x2 v2 = lds_tr16<16 * 256>(ad), v3 = lds_tr16<24 * 256>(ad);
+            lgkm_wait_tr(v0, v1, v2, v3);
+            u32x2 w0 = lds_tr16<32 * 256>(ad), w1 = lds_tr16<40 * 256>(ad);
+            u32x2 w2 = lds_tr16<48 * 256>(ad), w3 = lds_tr16<56 * 256>(ad);
+            const u32x4 va0 = {v0[0], v0[1], v1[0], v1[1]};
+            const u32x4 va1 = {v2[0], v2[1], v3[0], v3[1]};
+            o[nb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, va0), pb[0],
+                                                            o[nb], 0, 0, 0);
+            o[nb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, va1), pb[1],
+                                                            o[nb], 0, 0, 0);
+            lgkm_wait_tr(w0, w1, w2, w3);
+            const u32x4 va2 = {w0[0], w0[1], w1[0], w1[1]};
+            const u32x4 va3 = {w2[0], w2[1], w3[0], w3[1]};
+            o[nb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, va2), pb[2],
+                                                            o[nb], 0, 0, 0);
+            o[nb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, va3), pb[3],
+                                                            o[nb], 0, 0, 0);
+        }
+    };
+
+    if (ntiles > 0) {
+        load_map(0);
+        issue_tile(0, k_lds0, v_lds0);
+        if (ntiles > 1) load_map(1);
+    }
+    for (int t = 0; t < ntiles; ++t) {
+        // tile t lives in stage t & 1; tile t+1 streams into the other stage
+        unsigned char* kcur = (t & 1) ? k_lds1 : k_lds0;
+        unsigned char* vcur = (t & 1) ? v_lds1 : v_lds0;
+        unsigned char* knext = (t & 1) ? k_lds0 : k_lds1;
+        unsigned char* vnext = (t & 1) ? v_lds0 : v_lds1;
+        if (t + 1 < ntiles) {
+            issue_tile(t + 1, knext, vnext);
+            if (t + 2 < ntiles) load_map(t + 2);
+        }
+        wait_current(t + 1 < ntiles);
+        wg_barrier();
+        compute_tile(t, kcur, vcur);
+        wg_barrier();
     }
 
     store_rows<OutT>(a, c, q, hh, o, m_run, l_run);
