@@ -289,6 +289,12 @@ __device__ __forceinline__ void lgkm_wait2(u32x4& a, u32x4& b) {
     asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(a), "+v"(b)::"memory");
 }
 
+// Waits for all but the two most recent LDS reads (LDS reads complete in
+// issue order and no scalar-memory load is issued in the compute phase).
+__device__ __forceinline__ void lgkm_wait2_keep2(u32x4& a, u32x4& b) {
+    asm volatile("s_waitcnt lgkmcnt(2)" : "+v"(a), "+v"(b)::"memory");
+}
+
 __device__ __forceinline__ void lgkm_wait_tr(u32x2& a, u32x2& b, u32x2& c, u32x2& d) {
     asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(a), "+v"(b), "+v"(c), "+v"(d)::"memory");
 }
@@ -341,7 +347,7 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_bf16_kernel(AttnArgs a) 
 
     // KVMap entries of a tile are fetched one tile ahead of its K/V loads so
     // that their latency hides behind a tile of compute.
-    long mp[4] = {-1L, -1L, -1L, -1L};
+    int mp[4] = {-1, -1, -1, -1};
     auto load_map = [&](int t) {
         if (!map) return;
         const long t0 = kbeg + (long)t * kBf16BlockKeys;
@@ -349,24 +355,37 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_bf16_kernel(AttnArgs a) 
         for (int i = 0; i < 4; ++i) {
             long j = t0 + ld_row0 + 4 * i;
             if (j >= kend) j = kend - 1;
-            mp[i] = map[j];
+            const long m = map[j];
+            mp[i] = m >= 0 ? (int)(m < 0x7fffffffL ? m : 0x7fffffffL) : -1;
         }
     };
+    // Lane-constant byte offsets of the 16-byte chunk each lane copies.
+    unsigned kofs[4], vofs[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int row = ld_row0 + 4 * i;
+        kofs[i] = (unsigned)hoff_b + 16u * ((unsigned)ld_pch ^ (unsigned)(row & 15));
+        vofs[i] = (unsigned)hoff_b + 16u * ((unsigned)ld_pch ^ vswz(row));
+    }
+    const unsigned rb = (unsigned)row_bytes;
     auto issue_tile = [&](int t, unsigned char* kdst, unsigned char* vdst) {
         const long t0 = kbeg + (long)t * kBf16BlockKeys;
+        const bool full = t0 + kBf16BlockKeys <= kend;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const int row = ld_row0 + 4 * i;
             long j = t0 + row;
-            if (j >= kend) j = kend - 1;  // clamped rows are masked out of the softmax
-            const long m = mp[i];
-            const unsigned char* kp = m >= 0 ? Ab + m * 2 * row_bytes : Kb + j * row_bytes;
-            const unsigned char* vp = m >= 0 ? Ab + m * 2 * row_bytes + row_bytes : Vb + j * row_bytes;
-            const unsigned kc = (unsigned)ld_pch ^ (unsigned)(row & 15);
-            const unsigned vc = (unsigned)ld_pch ^ vswz(row);
-            __builtin_amdgcn_global_load_lds(kp + hoff_b + 16 * kc,
+            if (!full && j >= kend) j = kend - 1;  // clamped rows are masked out of the softmax
+            // Branch-free row address: arena row 2*m (K half) / 2*m+1 (V half)
+            // when the map says so, else row j of K / V.
+            const bool ar = mp[i] >= 0;
+            const unsigned idx = ar ? 2u * (unsigned)mp[i] : (unsigned)j;
+            const unsigned long off = (unsigned long)idx * rb;
+            const unsigned char* kbase = ar ? Ab : Kb;
+            const unsigned char* vbase = ar ? Ab + rb : Vb;
+            __builtin_amdgcn_global_load_lds(kbase + off + kofs[i],
                                              (KVP_LDS void*)(kdst + (4 * wave + i) * 1024), 16, 0, 0);
-            __builtin_amdgcn_global_load_lds(vp + hoff_b + 16 * vc,
+            __builtin_amdgcn_global_load_lds(vbase + off + vofs[i],
                                              (KVP_LDS void*)(vdst + (4 * wave + i) * 1024), 16, 0, 0);
         }
     };
@@ -408,21 +427,27 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_bf16_kernel(AttnArgs a) 
             s0[v] = 0.f;
             s1[v] = 0.f;
         }
-        // S^T = K Q^T, K fragments read two k-steps ahead of their MFMAs
-        u32x4 ka[2], kb[2];
-        {
-            const unsigned ad = kbase + ((((unsigned)hh) ^ kswz) << 4);
-            ka[0] = lds_b128<0>(ad);
-            kb[0] = lds_b128<32 * 256>(ad);
+        // S^T = K Q^T; K fragments are read two k-steps ahead of their MFMAs
+        // (lgkmcnt(2) leaves the newest pair in flight).
+        u32x4 ka[3], kb[3];
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks) {
+            const unsigned ad = kbase + ((((unsigned)(2 * ks + hh)) ^ kswz) << 4);
+            ka[ks] = lds_b128<0>(ad);
+            kb[ks] = lds_b128<32 * 256>(ad);
         }
 #pragma unroll
         for (int ks = 0; ks < 8; ++ks) {
-            const int cur = ks & 1;
-            lgkm_wait2(ka[cur], kb[cur]);
-            if (ks + 1 < 8) {
-                const unsigned ad = kbase + ((((unsigned)(2 * (ks + 1) + hh)) ^ kswz) << 4);
-                ka[cur ^ 1] = lds_b128<0>(ad);
-                kb[cur ^ 1] = lds_b128<32 * 256>(ad);
+            const int cur = ks % 3;
+            if (ks + 1 < 8)
+                lgkm_wait2_keep2(ka[cur], kb[cur]);
+            else
+                lgkm_wait2(ka[cur], kb[cur]);
+            if (ks + 2 < 8) {
+                const int nx = (ks + 2) % 3;
+                const unsigned ad = kbase + ((((unsigned)(2 * (ks + 2) + hh)) ^ kswz) << 4);
+                ka[nx] = lds_b128<0>(ad);
+                kb[nx] = lds_b128<32 * 256>(ad);
             }
             s0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, ka[cur]),
                                                          qf[ks], s0, 0, 0, 0);
@@ -664,51 +689,78 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_f32_kernel(AttnArgs a) {
 
 // ---------------------------------------------------------------------------
 // split combine: out[q, h, :] = sum_s w_s O_s / sum_s w_s, w_s = 2^(lse_s - M)
-// one thread per 4 output columns.
+// One thread per 8 output columns of one query row; every load of all splits
+// is issued before any arithmetic (MAXS bounds the unrolled split loop).
 // ---------------------------------------------------------------------------
-template <typename OutT>
+template <typename OutT, int MAXS>
 __global__ __launch_bounds__(256) void attn_combine_kernel(AttnArgs a) {
     const long gid = (long)blockIdx.x * blockDim.x + threadIdx.x;
-    const int cols4 = a.D / 4;
-    const long total = (long)a.frames * a.nq * cols4;
+    const int cols8 = a.D / 8;
+    const long total = (long)a.frames * a.nq * cols8;
     if (gid >= total) return;
-    const int c4 = (int)(gid % cols4);
-    const long rq = gid / cols4;
+    const int c8 = (int)(gid % cols8);
+    const long rq = gid / cols8;
     const int q = (int)(rq % a.nq);
     const int frame = (int)(rq / a.nq);
-    const int head = (4 * c4) / kHeadDim;
+    const int head = (8 * c8) / kHeadDim;
 
-    float mx = -INFINITY;
-    for (int s = 0; s < a.splits; ++s) {
-        const long slab = (long)s * a.frames + frame;
-        mx = fmaxf(mx, a.part_lse[(slab * a.heads + head) * (long)a.nq + q]);
+    float lse[MAXS];
+    f32x4 p0[MAXS], p1[MAXS];
+#pragma unroll
+    for (int s = 0; s < MAXS; ++s) {
+        if (s < a.splits) {
+            const long slab = (long)s * a.frames + frame;
+            lse[s] = a.part_lse[(slab * a.heads + head) * (long)a.nq + q];
+            const float* po = a.part_o + (slab * a.nq + q) * (long)a.D + 8 * c8;
+            p0[s] = *reinterpret_cast<const f32x4*>(po);
+            p1[s] = *reinterpret_cast<const f32x4*>(po + 4);
+        }
     }
+    float mx = lse[0];
+#pragma unroll
+    for (int s = 1; s < MAXS; ++s)
+        if (s < a.splits) mx = fmaxf(mx, lse[s]);
     float wsum = 0.f;
-    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-    for (int s = 0; s < a.splits; ++s) {
-        const long slab = (long)s * a.frames + frame;
-        const float w = fast_exp2(a.part_lse[(slab * a.heads + head) * (long)a.nq + q] - mx);
-        const f32x4 po = *reinterpret_cast<const f32x4*>(a.part_o + (slab * a.nq + q) * (long)a.D + 4 * c4);
-        wsum += w;
-        acc[0] = fmaf(w, po[0], acc[0]);
-        acc[1] = fmaf(w, po[1], acc[1]);
-        acc[2] = fmaf(w, po[2], acc[2]);
-        acc[3] = fmaf(w, po[3], acc[3]);
+    float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int s = 0; s < MAXS; ++s) {
+        if (s < a.splits) {
+            const float w = fast_exp2(lse[s] - mx);
+            wsum += w;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                acc[i] = fmaf(w, p0[s][i], acc[i]);
+                acc[4 + i] = fmaf(w, p1[s][i], acc[4 + i]);
+            }
+        }
     }
     const float inv = 1.0f / wsum;
-    OutT* out = reinterpret_cast<OutT*>(a.out) + (long)frame * a.q_fstride + (long)q * a.D + 4 * c4;
+    OutT* out = reinterpret_cast<OutT*>(a.out) + (long)frame * a.q_fstride + (long)q * a.D + 8 * c8;
     if constexpr (sizeof(OutT) == 4) {
-        f32x4 w = {acc[0] * inv, acc[1] * inv, acc[2] * inv, acc[3] * inv};
-        *reinterpret_cast<f32x4*>(out) = w;
+        const f32x4 w0 = {acc[0] * inv, acc[1] * inv, acc[2] * inv, acc[3] * inv};
+        const f32x4 w1 = {acc[4] * inv, acc[5] * inv, acc[6] * inv, acc[7] * inv};
+        *reinterpret_cast<f32x4*>(out) = w0;
+        *reinterpret_cast<f32x4*>(out + 4) = w1;
     } else {
-        typedef __attribute__((ext_vector_type(4))) __bf16 bf16x4;
-        bf16x4 w;
-        w[0] = (__bf16)(acc[0] * inv);
-        w[1] = (__bf16)(acc[1] * inv);
-        w[2] = (__bf16)(acc[2] * inv);
-        w[3] = (__bf16)(acc[3] * inv);
-        *reinterpret_cast<bf16x4*>(out) = w;
+        bf16x8 w;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) w[i] = (__bf16)(acc[i] * inv);
+        *reinterpret_cast<bf16x8*>(out) = w;
     }
+}
+
+template <typename OutT>
+void launch_combine(const AttnArgs& a, hipStream_t st) {
+    const long total = (long)a.frames * a.nq * (a.D / 8);
+    const dim3 grid((unsigned)((total + 255) / 256)), block(256);
+    if (a.splits <= 2)
+        hipLaunchKernelGGL((attn_combine_kernel<OutT, 2>), grid, block, 0, st, a);
+    else if (a.splits <= 4)
+        hipLaunchKernelGGL((attn_combine_kernel<OutT, 4>), grid, block, 0, st, a);
+    else if (a.splits <= 8)
+        hipLaunchKernelGGL((attn_combine_kernel<OutT, 8>), grid, block, 0, st, a);
+    else
+        hipLaunchKernelGGL((attn_combine_kernel<OutT, 16>), grid, block, 0, st, a);
 }
 
 // ---------------------------------------------------------------------------
@@ -848,6 +900,10 @@ int launch_attention(int dtype, const void* q, const void* k, const void* v, con
         set_error("attention: null q/k/v/out pointer");
         return 1;
     }
+    if (key_end > 0x7fffffffL || (long)frames * kv_fstride / (D > 0 ? D : 1) + key_end > 0x7fffffffL) {
+        set_error("attention: key rows must stay below 2^31");
+        return 1;
+    }
     if (kvmap && !arena) {
         set_error("attention: kvmap given without arena");
         return 1;
@@ -917,12 +973,10 @@ int launch_attention(int dtype, const void* q, const void* k, const void* v, con
         return 1;
     }
     if (p.splits > 1) {
-        const long total = (long)frames * nq * (D / 4);
-        const unsigned blocks = (unsigned)((total + 255) / 256);
         if (dtype == 1)
-            hipLaunchKernelGGL(attn_combine_kernel<__bf16>, dim3(blocks), dim3(256), 0, st, a);
+            launch_combine<__bf16>(a, st);
         else
-            hipLaunchKernelGGL(attn_combine_kernel<float>, dim3(blocks), dim3(256), 0, st, a);
+            launch_combine<float>(a, st);
         e = hipGetLastError();
         if (e != hipSuccess) {
             set_error("attention combine launch: %s", hipGetErrorString(e));

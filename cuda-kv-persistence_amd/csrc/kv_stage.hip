@@ -10,9 +10,9 @@
 // sizes are 16-byte aligned, byte moves otherwise. The map scatter rides in
 // trailing workgroups of the same launch.
 //
-// Descriptors travel through a pinned-host / device ring: each flush copies
-// its descriptors H2D asynchronously on the caller's stream; a ring region is
-// reused only after the event recorded behind its last user has completed.
+// Descriptors are read by the kernel straight from a ring of mapped pinned
+// host memory (no separate H2D copy); a ring region is reused only after the
+// event recorded behind the launch that read it has completed.
 
 #include <hip/hip_runtime.h>
 
@@ -91,8 +91,8 @@ __global__ __launch_bounds__(256) void stage_kernel(const KvpRowCopy* __restrict
 }
 
 struct Stager {
-    unsigned char* host = nullptr;
-    unsigned char* dev = nullptr;
+    unsigned char* host = nullptr;  // mapped pinned memory
+    unsigned char* dev = nullptr;   // device view of `host`
     size_t cap = 0;
     size_t head = 0;
     std::vector<hipEvent_t> inflight;
@@ -102,7 +102,6 @@ struct Stager {
         drain();
         for (hipEvent_t e : spare) (void)hipEventDestroy(e);
         if (host) (void)hipHostFree(host);
-        if (dev) (void)hipFree(dev);
     }
     bool drain() {
         bool ok = true;
@@ -118,20 +117,17 @@ struct Stager {
         if (need > cap) {
             if (!drain()) return false;
             if (host) (void)hipHostFree(host);
-            if (dev) (void)hipFree(dev);
             host = nullptr;
             dev = nullptr;
+            cap = 0;
             size_t want = need < ((size_t)4 << 20) ? ((size_t)4 << 20) : need * 2;
-            if (hipHostMalloc(reinterpret_cast<void**>(&host), want, hipHostMallocDefault) != hipSuccess) {
+            if (hipHostMalloc(reinterpret_cast<void**>(&host), want, hipHostMallocMapped) != hipSuccess) {
                 host = nullptr;
-                cap = 0;
                 return false;
             }
-            if (hipMalloc(reinterpret_cast<void**>(&dev), want) != hipSuccess) {
+            if (hipHostGetDevicePointer(reinterpret_cast<void**>(&dev), host, 0) != hipSuccess) {
                 (void)hipHostFree(host);
                 host = nullptr;
-                dev = nullptr;
-                cap = 0;
                 return false;
             }
             cap = want;
@@ -283,11 +279,6 @@ int kvp_stage_run(void* stager, void* arena, long row_stride_bytes, const KvpRow
         if (n_map > 0) {
             memcpy(h + copy_bytes, map_rows, (size_t)n_map * sizeof(long));
             memcpy(h + copy_bytes + map_bytes, map_slots, (size_t)n_map * sizeof(long));
-        }
-        hipError_t e = hipMemcpyAsync(d, h, need, hipMemcpyHostToDevice, hs);
-        if (e != hipSuccess) {
-            set_error("stage: descriptor upload: %s", hipGetErrorString(e));
-            return 1;
         }
         d_copies = reinterpret_cast<KvpRowCopy*>(d);
         d_rows = reinterpret_cast<long*>(d + copy_bytes);

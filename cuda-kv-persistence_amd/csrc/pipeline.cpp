@@ -11,11 +11,15 @@
 //   3. arena_begin_step, KVMap prefix [0, (f+1)*T) reset to -1, then every
 //      selected tile's rows staged in policy order, rows ascending, the map
 //      entry of each staged row set to its arena row / slot;
-//   4. one flush: device map rebuild + one gather launch for all copies;
+//   4. one flush = one launch: every row copy plus the KVMap entries that
+//      change (rows leaving the pinned set -> -1, new or moved rows -> slot);
 //   5. one attention launch for the frame.
-// Nothing synchronises the host per frame: staging, map rebuild and
-// attention are ordered on the pipeline's stream. The host map is kept for
-// introspection and plan-only use.
+// The device KVMap is never rebuilt from scratch: a host mirror of it gives
+// the exact difference to the map the reference driver would upload for this
+// frame (prefix reset to -1, then the staged rows), so after step 4 the
+// device map holds that map on the whole prefix (and -1 beyond it).
+// Nothing synchronises the host per frame: staging, map updates and
+// attention are ordered on the pipeline's stream.
 
 #include <algorithm>
 #include <cstring>
@@ -48,7 +52,12 @@ struct Pipeline {
     std::vector<long> ids;
     int count = 0;
     std::vector<char> selected, prev_selected;
-    std::vector<long> map_rows, map_slots;
+    std::vector<long> map_rows, map_slots;   // entries of this step
+    std::vector<long> dev_mirror;            // current device map content
+    std::vector<long> dev_rows;              // rows with a non-negative entry
+    std::vector<int> stamp;                  // step id that mapped a row
+    int step_id = 0;
+    std::vector<long> upd_rows, upd_vals;    // entries sent to the device
     long staged_tiles = 0;
     long copy_rows = 0;
     int next_frame = 0;
@@ -183,10 +192,30 @@ int step_frame(Pipeline& p, int f, const char* q, const char* k, const char* v, 
         if (all) ++p.staged_tiles;
     }
 
-    // 4. one flush: map rebuild + gather
+    // 4. one flush: row copies + changed map entries in one launch
     if (!p.plan_only) {
-        if (!mgr.flush_with_map(p.d_map, (long)(f + 1) * T, p.map_rows.data(),
-                                p.map_slots.data(), p.map_rows.size())) {
+        ++p.step_id;
+        p.upd_rows.clear();
+        p.upd_vals.clear();
+        for (size_t i = 0; i < p.map_rows.size(); ++i) {
+            const long r = p.map_rows[i];
+            p.stamp[(size_t)r] = p.step_id;
+            if (p.dev_mirror[(size_t)r] != p.map_slots[i]) {
+                p.upd_rows.push_back(r);
+                p.upd_vals.push_back(p.map_slots[i]);
+                p.dev_mirror[(size_t)r] = p.map_slots[i];
+            }
+        }
+        for (long r : p.dev_rows) {
+            if (p.stamp[(size_t)r] != p.step_id && p.dev_mirror[(size_t)r] != -1) {
+                p.upd_rows.push_back(r);
+                p.upd_vals.push_back(-1);
+                p.dev_mirror[(size_t)r] = -1;
+            }
+        }
+        p.dev_rows = p.map_rows;
+        if (!mgr.flush_with_map(p.d_map, 0, p.upd_rows.data(), p.upd_vals.data(),
+                                p.upd_rows.size())) {
             return 1;
         }
     }
@@ -274,8 +303,13 @@ void* kvp_pipeline_create(const char* policy, int cross, int streaming, int fram
         }
         p->h_map.assign((size_t)frames * T, -1L);
         if (!p->plan_only) {
-            p->d_map = static_cast<long*>(kvp_dev_alloc((size_t)frames * T * sizeof(long)));
+            const size_t n = (size_t)frames * T;
+            p->d_map = static_cast<long*>(kvp_dev_alloc(n * sizeof(long)));
             if (!p->d_map) return nullptr;
+            p->dev_mirror.assign(n, -1L);
+            p->stamp.assign(n, 0);
+            // the device map starts as all -1, matching the mirror
+            if (!p->mgr->flush_with_map(p->d_map, (long)n, nullptr, nullptr, 0)) return nullptr;
         }
     }
     return p.release();
