@@ -430,6 +430,10 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_bf16_kernel(AttnArgs a) 
         // S^T = K Q^T; K fragments are read two k-steps ahead of their MFMAs
         // (lgkmcnt(2) leaves the newest pair in flight).
         u32x4 ka[3], kb[3];
+        // MFMA sections run at raised wave priority: when both waves of a
+        // SIMD are ready, the one feeding the matrix core issues first and
+        // the other's softmax VALU work fills the gaps.
+        __builtin_amdgcn_s_setprio(1);
 #pragma unroll
         for (int ks = 0; ks < 2; ++ks) {
             const unsigned ad = kbase + ((((unsigned)(2 * ks + hh)) ^ kswz) << 4);
@@ -455,6 +459,7 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_bf16_kernel(AttnArgs a) 
                                                          qf[ks], s1, 0, 0, 0);
         }
 
+        __builtin_amdgcn_s_setprio(0);
         float s[32];
 #pragma unroll
         for (int v = 0; v < 16; ++v) {
@@ -512,6 +517,7 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_bf16_kernel(AttnArgs a) 
         // O^T += V^T P^T; transposed V reads of rows 16g + 4hh + s and +8
         // (row offsets 16g*256 and 8*256 are immediates).
         const unsigned vbase = (unsigned)(uintptr_t)vt_lds + (unsigned)((4 * hh + tr_s) * 256 + vsub);
+        __builtin_amdgcn_s_setprio(1);
 #pragma unroll
         for (int nb = 0; nb < 4; ++nb) {
             const unsigned ad = vbase + ((((unsigned)(4 * nb) | vcl) ^ vs) << 4);
@@ -534,6 +540,7 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_bf16_kernel(AttnArgs a) 
             o[nb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, va3), pb[3],
                                                             o[nb], 0, 0, 0);
         }
+        __builtin_amdgcn_s_setprio(0);
     };
 
     if (ntiles > 0) {
@@ -831,8 +838,10 @@ void* workspace(int dev, size_t bytes) {
 }
 
 // Estimated time in units of one key tile processed by a full wave of
-// workgroups. Splitting divides the per-workgroup key loop but adds a
-// combine pass whose cost grows with the number of splits.
+// workgroups. Splitting divides the per-workgroup key loop but every split
+// writes and the combine re-reads one fp32 partial of the whole output
+// (about one tile-round of time per split at the C3 shape, measured), plus a
+// fixed cost for the extra launch.
 int choose_splits(long base_wg, long ntiles, long slots) {
     if (slots <= 0) slots = 512;
     int best = 1;
@@ -843,7 +852,7 @@ int choose_splits(long base_wg, long ntiles, long slots) {
         const long rounds = (wgs + slots - 1) / slots;
         const long per = (ntiles + s - 1) / s;
         double t = (double)rounds * (double)per;
-        if (s > 1) t += 2.0 + 0.5 * (double)s * (double)base_wg / (double)slots;
+        if (s > 1) t += 2.0 + 1.2 * (double)s * (double)base_wg / 156.0;
         if (t < best_t - 1e-9) {
             best_t = t;
             best = s;
