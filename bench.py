@@ -50,6 +50,12 @@ def parse():
                     help="frame-units of the CPU baseline sample (frames 0..1 of one layer = 3)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--streaming", action="store_true", help="sticky-slot arena mode")
+    ap.add_argument("--profile-policy", default=None,
+                    help="run exactly one 30-layer step of this policy's pipeline and exit "
+                         "(for rocprofv3 --pmc byte counting per policy)")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="run 4 device-to-device copies of 256 MiB and exit (known-size "
+                         "reference for FETCH_SIZE / WRITE_SIZE scaling)")
     return ap.parse_args()
 
 
@@ -101,6 +107,16 @@ def main():
     lib = _lib.load()
     assert torch.cuda.is_available(), "bench needs a GPU"
     dev = torch.device("cuda:0")
+    if args.copy_calibration:
+        nbytes = 256 << 20
+        src = torch.ones(nbytes // 4, device=dev)
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        for _ in range(4):
+            assert lib.kvp_memcpy_d2d(dst.data_ptr(), src.data_ptr(), nbytes, None) == 0
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_calibration_bytes_per_copy": nbytes, "copies": 4}), flush=True)
+        return
     cfg = workloads.CONFIGS["c3"]
     layers = args.layers
     T, D, H, F = cfg.tokens, workloads.HIDDEN, workloads.HEADS, cfg.frames
@@ -136,6 +152,16 @@ def main():
         torch.cuda.synchronize()
         wall = (time.perf_counter() - t0) * 1e3
         return e0.elapsed_time(e1) / steps, wall / steps
+
+    if args.profile_policy:
+        pl = make(args.profile_policy)
+        torch.cuda.synchronize()
+        run_step(pl)
+        torch.cuda.synchronize()
+        pl.close()
+        print(json.dumps({"profile_policy": args.profile_policy, "layers": layers,
+                          "frames": F, "query_frames": layers * F}), flush=True)
+        return
 
     # --- headline: policy pipeline, K timed steps -----------------------------------
     main_pl = make(args.policy)
@@ -190,12 +216,22 @@ def main():
         policies[pol]["attn_kernel_ms_per_frame"] = round(per_frame_attn, 4)
     log(f"attention kernels: {attn_ms:.3f} ms over {launches} launches, {achieved:.1f} TFLOP/s")
 
+    # Fabric bytes come from rocprofv3 FETCH_SIZE / WRITE_SIZE runs of this same
+    # workload (bench.py --profile-policy P), scaled by a copy-kernel calibration
+    # and committed under profiles/; counters cannot be read from inside a run.
     traffic = None
     tfile = ROOT / "profiles" / "attn_bf16_c3_traffic.json"
     if tfile.exists():
         try:
-            traffic = json.loads(tfile.read_text()).get("hbm_bytes_per_launch")
-        except Exception:
+            tj = json.loads(tfile.read_text())
+            traffic = tj.get("hbm_bytes_per_launch")
+            for pol, rec in tj.get("policies", {}).items():
+                if pol in policies:
+                    policies[pol]["attn_read_bytes_per_frame"] = rec.get("attn_read_bytes_per_frame")
+                    policies[pol]["attn_read_delta_vs_none"] = rec.get("attn_read_delta_vs_none")
+                    policies[pol]["all_kernels_read_bytes_per_frame"] = rec.get(
+                        "all_kernels_read_bytes_per_frame")
+        except (OSError, ValueError):
             traffic = None
 
     cpu = None
