@@ -206,8 +206,8 @@ __device__ __forceinline__ float softmax_update(float (&s)[N], float scale_log2,
 // bf16 kernel
 //
 // K and V tiles (64 keys x 128 dims, 16 KiB each) stream global -> LDS with
-// global_load_lds_dwordx4 (no register staging) into a two-stage ring: the
-// loads of tile t+1 are in flight while tile t is computed. Lane l of the
+// buffer_load_dwordx4 ... lds (no register staging) into a two-stage ring:
+// the loads of tile t+1 are in flight while tile t is computed. Lane l of the
 // wave's load instruction writes LDS bytes [base + 16*l, +16); it picks the
 // global 16-byte chunk that belongs at that (swizzled) LDS position.
 //
@@ -223,14 +223,20 @@ __device__ __forceinline__ float softmax_update(float (&s)[N], float scale_log2,
 // 0..3. That yields the V^T operand of O^T = V^T P^T directly.
 //
 // Softmax: scores stay in the log2 domain (scale folded into one FMA before
-// v_exp_f32). The running max used for exponentiation is only raised when a
-// lane's tile max exceeds it by more than kLazyRescale (2^8): O and l are then
-// rescaled together (wave-uniform branch). Until then p <= 2^8, exact in
-// fp32/bf16 range, and O/l is unchanged mathematically.
+// v_exp_f32). Exponentials are taken against the running max without
+// computing the tile max; the running max is raised (and O, l rescaled
+// together, wave-uniform branch) only when a row sum would exceed 2^64 or is
+// not finite — on the first tile and on strong score growth. O/l is
+// unchanged mathematically; p stays within bf16/fp32 range.
 // ---------------------------------------------------------------------------
 
 constexpr int kBf16TileBytes = kBf16BlockKeys * kHeadDim * 2;  // 16 KiB
-constexpr float kLazyRescale = 8.0f;
+// Raw buffer descriptor word 3 for gfx9-family (32-bit data format, no
+// swizzle): out-of-range offsets (>= num_records) read as zero.
+constexpr int kBufFlags = 0x00020000;
+// Row-sum bound of one tile's exponentials (2^64): below it every p fits
+// bf16/fp32 comfortably and O, l accumulate without rescaling.
+constexpr float kRowSumLimit = 18446744073709551616.0f;
 constexpr unsigned kVSwzTable = 0xAC60u;  // nibbles {0, 6, 12, 10}
 
 typedef __attribute__((ext_vector_type(4))) short v4i16;
@@ -340,58 +346,77 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_bf16_kernel(AttnArgs a) 
         __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
     }
 
-    // Load assignment: instruction i of wave w fills LDS bytes [(4w+i)*1 KiB, +1 KiB)
+    // Copy assignment: instruction i of wave w fills LDS bytes [(4w+i)*1 KiB, +1 KiB)
     // of each tile: rows 16w + 4i + lane/16, physical chunk lane % 16.
+    // Copies are buffer loads straight into LDS. Per tile, the K/V buffer
+    // descriptors are based at the tile's first key row and cover only rows
+    // below kend, so rows past the end read as zeros (they are masked out of
+    // the softmax) without any per-lane clamping; lane offsets are constant
+    // across tiles. Arena rows (KVMap >= 0) go through an arena descriptor.
     const int ld_row0 = 16 * wave + (lane >> 4);
     const int ld_pch = lane & 15;
+    const unsigned rb = (unsigned)row_bytes;
+    // Rows ld_row0 + 4i: (row & 15) repeats with period 4 in i and (row & 3)
+    // is the same for every i.
+    unsigned kofs[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+        kofs[i] = (unsigned)hoff_b + 16u * ((unsigned)ld_pch ^ (unsigned)((ld_row0 + 4 * i) & 15));
+    const unsigned vofs = (unsigned)hoff_b + 16u * ((unsigned)ld_pch ^ vswz(ld_row0));
+    const unsigned lane_row = (unsigned)ld_row0 * rb;
+    const __amdgpu_buffer_rsrc_t arena_rs =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<unsigned char*>(Ab), (short)0, -1, kBufFlags);
 
-    // KVMap entries of a tile are fetched one tile ahead of its K/V loads so
-    // that their latency hides behind a tile of compute.
-    int mp[4] = {-1, -1, -1, -1};
+    // KVMap entries of a tile are fetched one tile ahead of its copies and
+    // decoded when the copies are issued. Memory counters retire in issue
+    // order, so that decode also waits for the copies of the tile in between;
+    // those are waited for right after anyway, before that tile is computed.
+    // Any negative entry, or one of 2^31 or more, reads the original K/V row.
+    u32x2 mraw[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) mraw[i] = u32x2{0xffffffffu, 0xffffffffu};
     auto load_map = [&](int t) {
         if (!map) return;
         const long t0 = kbeg + (long)t * kBf16BlockKeys;
+        const long left = kend - t0;
+        const int nrec = (int)((left < kBf16BlockKeys ? left : kBf16BlockKeys) * 8);
+        const __amdgpu_buffer_rsrc_t mrs = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<long*>(map + t0), (short)0, nrec, kBufFlags);
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            long j = t0 + ld_row0 + 4 * i;
-            if (j >= kend) j = kend - 1;
-            const long m = map[j];
-            mp[i] = m >= 0 ? (int)(m < 0x7fffffffL ? m : 0x7fffffffL) : -1;
+            mraw[i] = __builtin_amdgcn_raw_buffer_load_b64(mrs, (unsigned)(ld_row0 + 4 * i) * 8u, 0, 0);
         }
     };
-    // Lane-constant byte offsets of the 16-byte chunk each lane copies.
-    unsigned kofs[4], vofs[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const int row = ld_row0 + 4 * i;
-        kofs[i] = (unsigned)hoff_b + 16u * ((unsigned)ld_pch ^ (unsigned)(row & 15));
-        vofs[i] = (unsigned)hoff_b + 16u * ((unsigned)ld_pch ^ vswz(row));
-    }
-    const unsigned rb = (unsigned)row_bytes;
     auto issue_tile = [&](int t, unsigned char* kdst, unsigned char* vdst) {
         const long t0 = kbeg + (long)t * kBf16BlockKeys;
-        const bool full = t0 + kBf16BlockKeys <= kend;
+        const long left = kend - t0;
+        const int nrec = (int)((left < kBf16BlockKeys ? left : kBf16BlockKeys) * (long)rb);
+        const __amdgpu_buffer_rsrc_t krs = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<unsigned char*>(Kb + t0 * (long)rb), (short)0, nrec, kBufFlags);
+        const __amdgpu_buffer_rsrc_t vrs = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<unsigned char*>(Vb + t0 * (long)rb), (short)0, nrec, kBufFlags);
+        const unsigned koff = (unsigned)__builtin_amdgcn_readfirstlane((int)(uintptr_t)kdst) + 4096u * wave;
+        const unsigned voff = (unsigned)__builtin_amdgcn_readfirstlane((int)(uintptr_t)vdst) + 4096u * wave;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            const int row = ld_row0 + 4 * i;
-            long j = t0 + row;
-            if (!full && j >= kend) j = kend - 1;  // clamped rows are masked out of the softmax
-            // Branch-free row address: arena row 2*m (K half) / 2*m+1 (V half)
-            // when the map says so, else row j of K / V.
-            const bool ar = mp[i] >= 0;
-            const unsigned idx = ar ? 2u * (unsigned)mp[i] : (unsigned)j;
-            const unsigned long off = (unsigned long)idx * rb;
-            const unsigned char* kbase = ar ? Ab : Kb;
-            const unsigned char* vbase = ar ? Ab + rb : Vb;
-            __builtin_amdgcn_global_load_lds(kbase + off + kofs[i],
-                                             (KVP_LDS void*)(kdst + (4 * wave + i) * 1024), 16, 0, 0);
-            __builtin_amdgcn_global_load_lds(vbase + off + vofs[i],
-                                             (KVP_LDS void*)(vdst + (4 * wave + i) * 1024), 16, 0, 0);
+            KVP_LDS void* kd = (KVP_LDS void*)(uintptr_t)(koff + 1024u * i);
+            KVP_LDS void* vd = (KVP_LDS void*)(uintptr_t)(voff + 1024u * i);
+            const unsigned row_off = lane_row + 4u * i * rb;
+            // arena row = the map word when it is a non-negative value below 2^31
+            const bool in_arena = map && mraw[i][1] == 0u && (int)mraw[i][0] >= 0;
+            if (in_arena) {
+                const unsigned ao = 2u * mraw[i][0] * rb;
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(arena_rs, kd, 16, ao + kofs[i], 0, 0, 0);
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(arena_rs, vd, 16, ao + rb + vofs, 0, 0, 0);
+            } else {
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(krs, kd, 16, row_off + kofs[i], 0, 0, 0);
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(vrs, vd, 16, row_off + vofs, 0, 0, 0);
+            }
         }
     };
-    // Waits until the K/V loads of the tile about to be computed have landed:
-    // the next tile's 8 loads (and, with a map, 4 prefetched map loads) may
-    // still be in flight.
+    // Waits until the copies of the tile about to be computed have landed.
+    // Issued after them: the 4 map loads of the next tile (with a map) and
+    // the 8 copies of the next tile; those stay in flight.
     auto wait_current = [&](bool more) {
         if (!more)
             wait_vm<0>();
@@ -476,43 +501,49 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_bf16_kernel(AttnArgs a) 
             }
         }
 
-        // row max over this tile (both lane halves hold disjoint keys)
-        float mx = fmaxf(fmaxf(s[0], s[1]), s[2]);
+        // Exponentiate against the running max; only when the tile's row sum
+        // overflows the bound (first tile, where the running max is -inf, or
+        // scores that grew far beyond it) take the slow path: raise the max
+        // to the tile max, rescale O and l, and exponentiate again.
+        bf16x8 pb[4];
+        auto exp_tile = [&](float mref) {
+            float rs = 0.f;
 #pragma unroll
-        for (int v = 3; v < 31; v += 2) mx = fmaxf(fmaxf(mx, s[v]), s[v + 1]);
-        mx = fmaxf(mx, s[31]);
-        float mlo, mhi;
-        swap_halves(mx, mlo, mhi);
-        mx = fmaxf(mlo, mhi) * cl2;
-        if (__builtin_amdgcn_ballot_w64(mx > m_run + kLazyRescale)) {
-            const float m_new = fmaxf(m_run, mx);
-            const float corr = fast_exp2(m_run - m_new);
+            for (int g = 0; g < 4; ++g) {
+#pragma unroll
+                for (int i = 0; i < 8; i += 2) {
+                    bf16x2 pr;
+                    pr[0] = (__bf16)fast_exp2(fmaf(s[8 * g + i], cl2, -mref));
+                    pr[1] = (__bf16)fast_exp2(fmaf(s[8 * g + i + 1], cl2, -mref));
+                    pb[g][i] = pr[0];
+                    pb[g][i + 1] = pr[1];
+                    const bf16x2 one = {(__bf16)1.0f, (__bf16)1.0f};
+                    rs = __builtin_amdgcn_fdot2_f32_bf16(pr, one, rs, false);
+                }
+            }
+            float rlo, rhi;
+            swap_halves(rs, rlo, rhi);
+            return rlo + rhi;
+        };
+        float tot = exp_tile(m_run);
+        if (__builtin_amdgcn_ballot_w64(!(tot <= kRowSumLimit))) {
+            float mx = fmaxf(fmaxf(s[0], s[1]), s[2]);
+#pragma unroll
+            for (int v = 3; v < 31; v += 2) mx = fmaxf(fmaxf(mx, s[v]), s[v + 1]);
+            mx = fmaxf(mx, s[31]);
+            float mlo, mhi;
+            swap_halves(mx, mlo, mhi);
+            const float m_new = fmaxf(m_run, fmaxf(mlo, mhi) * cl2);
+            const float corr = fast_exp2(m_run - m_new);  // 0 while m_run is -inf
             l_run *= corr;
 #pragma unroll
             for (int nb = 0; nb < 4; ++nb)
 #pragma unroll
                 for (int v = 0; v < 16; ++v) o[nb][v] *= corr;
             m_run = m_new;
+            tot = exp_tile(m_run);
         }
-
-        bf16x8 pb[4];
-        float rs = 0.f;
-#pragma unroll
-        for (int g = 0; g < 4; ++g) {
-#pragma unroll
-            for (int i = 0; i < 8; i += 2) {
-                bf16x2 pr;
-                pr[0] = (__bf16)fast_exp2(fmaf(s[8 * g + i], cl2, -m_run));
-                pr[1] = (__bf16)fast_exp2(fmaf(s[8 * g + i + 1], cl2, -m_run));
-                pb[g][i] = pr[0];
-                pb[g][i + 1] = pr[1];
-                const bf16x2 one = {(__bf16)1.0f, (__bf16)1.0f};
-                rs = __builtin_amdgcn_fdot2_f32_bf16(pr, one, rs, false);
-            }
-        }
-        float rlo, rhi;
-        swap_halves(rs, rlo, rhi);
-        l_run += rlo + rhi;
+        l_run += tot;
 
         // O^T += V^T P^T; transposed V reads of rows 16g + 4hh + s and +8
         // (row offsets 16g*256 and 8*256 are immediates).
