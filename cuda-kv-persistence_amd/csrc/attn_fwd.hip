@@ -285,6 +285,13 @@ __device__ __forceinline__ u32x4 lds_b128(unsigned addr) {
 }
 
 template <int OFF>
+__device__ __forceinline__ u32x2 lds_b64(unsigned addr) {
+    u32x2 r;
+    asm volatile("ds_read_b64 %0, %1 offset:%2" : "=v"(r) : "v"(addr), "n"(OFF) : "memory");
+    return r;
+}
+
+template <int OFF>
 __device__ __forceinline__ u32x2 lds_tr16(unsigned addr) {
     u32x2 r;
     asm volatile("ds_read_b64_tr_b16 %0, %1 offset:%2" : "=v"(r) : "v"(addr), "n"(OFF) : "memory");
@@ -311,6 +318,9 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_bf16_kernel(AttnArgs a) 
     __shared__ __attribute__((aligned(1024))) unsigned char v_lds0[kBf16TileBytes];
     __shared__ __attribute__((aligned(1024))) unsigned char k_lds1[kBf16TileBytes];
     __shared__ __attribute__((aligned(1024))) unsigned char v_lds1[kBf16TileBytes];
+    // KVMap words of a tile: 2 tile slots x 4 waves x 256 bytes; each wave
+    // copies and reads only its own 256 bytes.
+    __shared__ __attribute__((aligned(256))) unsigned char m_lds[2 * 4 * 256];
 
     const WgCoord c = decode_wg(a);
     const int tid = threadIdx.x;
@@ -367,14 +377,34 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_bf16_kernel(AttnArgs a) 
     const __amdgpu_buffer_rsrc_t arena_rs =
         __builtin_amdgcn_make_buffer_rsrc(const_cast<unsigned char*>(Ab), (short)0, -1, kBufFlags);
 
-    // KVMap entries of a tile are fetched one tile ahead of its copies and
-    // decoded when the copies are issued. Memory counters retire in issue
-    // order, so that decode also waits for the copies of the tile in between;
-    // those are waited for right after anyway, before that tile is computed.
-    // Any negative entry, or one of 2^31 or more, reads the original K/V row.
-    u32x2 mraw[4];
+    // KVMap entries of a tile are copied into LDS two tiles ahead (one
+    // 4-byte copy per lane: wave w takes the tile's rows 16w.. as 32 words;
+    // lanes past the tile's end read zeros), before the copies of the tile in
+    // between. Right before the tile's own K/V copies are issued they are
+    // decoded into arena byte offsets; memory counters retire in issue order,
+    // so that decode waits on the map copy alone while the copies of the tile
+    // in between stay in flight. Any negative entry, or one of 2^31 or more,
+    // reads the original K/V row (offset ~0u).
+    const unsigned m_wave = (unsigned)(uintptr_t)m_lds + 256u * wave;
+    unsigned mdec[4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) mraw[i] = u32x2{0xffffffffu, 0xffffffffu};
+    for (int i = 0; i < 4; ++i) mdec[i] = ~0u;
+    // map copy of tile `t` outstanding behind exactly `behind` later vector
+    // memory operations
+    auto decode_map = [&](int t, bool behind8) {
+        if (!map) return;
+        if (behind8)
+            wait_vm<8>();
+        else
+            wait_vm<0>();
+        const unsigned ad = m_wave + 1024u * (unsigned)(t & 1) + 8u * (unsigned)(lane >> 4);
+        u32x2 m0 = lds_b64<0>(ad), m1 = lds_b64<32>(ad), m2 = lds_b64<64>(ad), m3 = lds_b64<96>(ad);
+        lgkm_wait_tr(m0, m1, m2, m3);
+        const u32x2 mw[4] = {m0, m1, m2, m3};
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            mdec[i] = (mw[i][1] == 0u && (int)mw[i][0] >= 0) ? 2u * mw[i][0] * rb : ~0u;
+    };
     auto load_map = [&](int t) {
         if (!map) return;
         const long t0 = kbeg + (long)t * kBf16BlockKeys;
@@ -382,10 +412,9 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_bf16_kernel(AttnArgs a) 
         const int nrec = (int)((left < kBf16BlockKeys ? left : kBf16BlockKeys) * 8);
         const __amdgpu_buffer_rsrc_t mrs = __builtin_amdgcn_make_buffer_rsrc(
             const_cast<long*>(map + t0), (short)0, nrec, kBufFlags);
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            mraw[i] = __builtin_amdgcn_raw_buffer_load_b64(mrs, (unsigned)(ld_row0 + 4 * i) * 8u, 0, 0);
-        }
+        KVP_LDS void* md = (KVP_LDS void*)(uintptr_t)(
+            (unsigned)__builtin_amdgcn_readfirstlane((int)m_wave) + 1024u * (unsigned)(t & 1));
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(mrs, md, 4, 128u * wave + 4u * lane, 0, 0, 0);
     };
     auto issue_tile = [&](int t, unsigned char* kdst, unsigned char* vdst) {
         const long t0 = kbeg + (long)t * kBf16BlockKeys;
@@ -402,10 +431,8 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_bf16_kernel(AttnArgs a) 
             KVP_LDS void* kd = (KVP_LDS void*)(uintptr_t)(koff + 1024u * i);
             KVP_LDS void* vd = (KVP_LDS void*)(uintptr_t)(voff + 1024u * i);
             const unsigned row_off = lane_row + 4u * i * rb;
-            // arena row = the map word when it is a non-negative value below 2^31
-            const bool in_arena = map && mraw[i][1] == 0u && (int)mraw[i][0] >= 0;
-            if (in_arena) {
-                const unsigned ao = 2u * mraw[i][0] * rb;
+            if (map && mdec[i] != ~0u) {
+                const unsigned ao = mdec[i];
                 __builtin_amdgcn_raw_ptr_buffer_load_lds(arena_rs, kd, 16, ao + kofs[i], 0, 0, 0);
                 __builtin_amdgcn_raw_ptr_buffer_load_lds(arena_rs, vd, 16, ao + rb + vofs, 0, 0, 0);
             } else {
@@ -415,13 +442,14 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_bf16_kernel(AttnArgs a) 
         }
     };
     // Waits until the copies of the tile about to be computed have landed.
-    // Issued after them: the 4 map loads of the next tile (with a map) and
-    // the 8 copies of the next tile; those stay in flight.
-    auto wait_current = [&](bool more) {
+    // Issued after them: the map copy of the tile after next (when a map is
+    // read and that tile exists) and the 8 copies of the next tile; those
+    // stay in flight.
+    auto wait_current = [&](bool more, bool map_ahead) {
         if (!more)
             wait_vm<0>();
-        else if (map)
-            wait_vm<12>();
+        else if (map_ahead)
+            wait_vm<9>();
         else
             wait_vm<8>();
     };
@@ -576,8 +604,9 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_bf16_kernel(AttnArgs a) 
 
     if (ntiles > 0) {
         load_map(0);
-        issue_tile(0, k_lds0, v_lds0);
+        decode_map(0, false);
         if (ntiles > 1) load_map(1);
+        issue_tile(0, k_lds0, v_lds0);
     }
     for (int t = 0; t < ntiles; ++t) {
         // tile t lives in stage t & 1; tile t+1 streams into the other stage
@@ -585,11 +614,13 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_bf16_kernel(AttnArgs a) 
         unsigned char* vcur = (t & 1) ? v_lds1 : v_lds0;
         unsigned char* knext = (t & 1) ? k_lds0 : k_lds1;
         unsigned char* vnext = (t & 1) ? v_lds0 : v_lds1;
+        const bool map_ahead = map && t + 2 < ntiles;
         if (t + 1 < ntiles) {
+            decode_map(t + 1, true);
+            if (map_ahead) load_map(t + 2);
             issue_tile(t + 1, knext, vnext);
-            if (t + 2 < ntiles) load_map(t + 2);
         }
-        wait_current(t + 1 < ntiles);
+        wait_current(t + 1 < ntiles, map_ahead);
         wg_barrier();
         compute_tile(t, kcur, vcur);
         wg_barrier();
