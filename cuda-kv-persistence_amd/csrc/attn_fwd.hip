@@ -43,6 +43,7 @@
 
 #include "kvp_c_api.h"
 #include "kvp_internal.h"
+#include "stage_runs.h"
 
 namespace kvp {
 namespace {
@@ -762,8 +763,8 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_f32_kernel(AttnArgs a) {
 // is issued before any arithmetic (MAXS bounds the unrolled split loop).
 // ---------------------------------------------------------------------------
 template <typename OutT, int MAXS>
-__global__ __launch_bounds__(256) void attn_combine_kernel(AttnArgs a) {
-    const long gid = (long)blockIdx.x * blockDim.x + threadIdx.x;
+__device__ __forceinline__ void combine_block(const AttnArgs& a, long block) {
+    const long gid = block * 256 + threadIdx.x;
     const int cols8 = a.D / 8;
     const long total = (long)a.frames * a.nq * cols8;
     if (gid >= total) return;
@@ -818,10 +819,43 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(AttnArgs a) {
     }
 }
 
+template <typename OutT, int MAXS>
+__global__ __launch_bounds__(256) void attn_combine_kernel(AttnArgs a) {
+    combine_block<OutT, MAXS>(a, blockIdx.x);
+}
+
+// The combine followed by a staging flush in the same launch: workgroups
+// [0, combine_blocks) merge the partials, the rest run the flush (it may
+// overwrite arena rows and KVMap entries: the attention kernel that read
+// them has completed before this launch starts).
+template <typename OutT, int MAXS>
+__global__ __launch_bounds__(256) void attn_combine_stage_kernel(AttnArgs a, stage::RunArgs r,
+                                                                 int combine_blocks) {
+    const int b = blockIdx.x;
+    if (b < combine_blocks)
+        combine_block<OutT, MAXS>(a, b);
+    else
+        stage::stage_runs_block(r, b - combine_blocks);
+}
+
 template <typename OutT>
-void launch_combine(const AttnArgs& a, hipStream_t st) {
+void launch_combine(const AttnArgs& a, hipStream_t st, const stage::RunArgs* follow) {
     const long total = (long)a.frames * a.nq * (a.D / 8);
-    const dim3 grid((unsigned)((total + 255) / 256)), block(256);
+    const long cblocks = (total + 255) / 256;
+    const dim3 block(256);
+    if (follow) {
+        const dim3 grid((unsigned)(cblocks + stage::run_blocks(*follow)));
+        if (a.splits <= 2)
+            hipLaunchKernelGGL((attn_combine_stage_kernel<OutT, 2>), grid, block, 0, st, a, *follow, (int)cblocks);
+        else if (a.splits <= 4)
+            hipLaunchKernelGGL((attn_combine_stage_kernel<OutT, 4>), grid, block, 0, st, a, *follow, (int)cblocks);
+        else if (a.splits <= 8)
+            hipLaunchKernelGGL((attn_combine_stage_kernel<OutT, 8>), grid, block, 0, st, a, *follow, (int)cblocks);
+        else
+            hipLaunchKernelGGL((attn_combine_stage_kernel<OutT, 16>), grid, block, 0, st, a, *follow, (int)cblocks);
+        return;
+    }
+    const dim3 grid((unsigned)cblocks);
     if (a.splits <= 2)
         hipLaunchKernelGGL((attn_combine_kernel<OutT, 2>), grid, block, 0, st, a);
     else if (a.splits <= 4)
@@ -951,6 +985,14 @@ int launch_attention(int dtype, const void* q, const void* k, const void* v, con
                      const long* kvmap, void* out, int nq, int D, int heads, int frames,
                      long q_fstride, long kv_fstride, long map_fstride, long key_begin,
                      long key_end, void* stream) {
+    return launch_attention(dtype, q, k, v, arena, kvmap, out, nq, D, heads, frames, q_fstride,
+                            kv_fstride, map_fstride, key_begin, key_end, stream, nullptr);
+}
+
+int launch_attention(int dtype, const void* q, const void* k, const void* v, const void* arena,
+                     const long* kvmap, void* out, int nq, int D, int heads, int frames,
+                     long q_fstride, long kv_fstride, long map_fstride, long key_begin,
+                     long key_end, void* stream, const void* follow) {
     if (dtype != 0 && dtype != 1) {
         set_error("attention: dtype %d not supported (0 = fp32, 1 = bf16)", dtype);
         return 1;
@@ -1044,17 +1086,19 @@ int launch_attention(int dtype, const void* q, const void* k, const void* v, con
         return 1;
     }
     if (p.splits > 1) {
+        const stage::RunArgs* carried = static_cast<const stage::RunArgs*>(stage_plan_runs(follow));
         if (dtype == 1)
-            launch_combine<__bf16>(a, st);
+            launch_combine<__bf16>(a, st, carried);
         else
-            launch_combine<float>(a, st);
+            launch_combine<float>(a, st, carried);
         e = hipGetLastError();
         if (e != hipSuccess) {
             set_error("attention combine launch: %s", hipGetErrorString(e));
             return 1;
         }
+        if (carried) return 0;
     }
-    return 0;
+    return follow ? stage_plan_launch(follow, stream) : 0;
 }
 
 int attention_splits(int dtype, int nq, int heads, int frames, long span) {

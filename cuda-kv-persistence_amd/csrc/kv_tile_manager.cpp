@@ -6,6 +6,7 @@
 // and no L2 persistence state exists on CDNA4.
 
 #include "kv_tile_manager.h"
+#include "kvp_internal.h"
 
 #include <cstdint>
 #include <cstdio>
@@ -165,6 +166,24 @@ bool KVTileManager::flush_with_map(long* map_dev, long map_fill,
     pending_.clear();
     pending_by_row_.clear();
     return rc == 0;
+}
+
+bool KVTileManager::flush_plan(void** plan, long* map_dev, long map_fill, const long* map_rows,
+                               const long* map_slots, size_t n_map) const {
+    *plan = nullptr;
+    if (plan_only_) return true;
+    if (pending_.empty() && !map_dev) return true;
+    KVTileManager* self = const_cast<KVTileManager*>(this);
+    if (!self->stager_) {
+        self->stager_ = kvp_stager_create();
+        if (!self->stager_) return false;
+    }
+    *plan = kvp::stage_plan_create(stager_, arena_, (long)(arena_row_stride_floats_ * sizeof(float)),
+                                   pending_.data(), (long)pending_.size(), map_dev, map_fill, map_rows,
+                                   map_slots, (long)n_map);
+    pending_.clear();
+    pending_by_row_.clear();
+    return *plan != nullptr;
 }
 
 // reference: src/kv_tile_manager.cu:104-121 — both gates use the running

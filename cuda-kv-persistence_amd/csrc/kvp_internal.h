@@ -4,6 +4,8 @@
 
 #include <cstddef>
 
+#include "kvp_c_api.h"
+
 namespace kvp {
 
 // Record a failure for kvp_last_error() (thread-local text).
@@ -23,6 +25,28 @@ int launch_attention(int dtype, const void* q, const void* k, const void* v,
                      long kv_fstride, long map_fstride, long key_begin,
                      long key_end, void* stream);
 
+// Same, followed on the stream by a prepared staging flush (see below): the
+// flush runs as trailing workgroups of the split-combine launch when there
+// is one and the flush is argument-encoded, else as its own launch right
+// after the attention launch. follow may be null.
+int launch_attention(int dtype, const void* q, const void* k, const void* v,
+                     const void* arena, const long* kvmap, void* out, int nq,
+                     int D, int heads, int frames, long q_fstride,
+                     long kv_fstride, long map_fstride, long key_begin,
+                     long key_end, void* stream, const void* follow);
+
 int attention_splits(int dtype, int nq, int heads, int frames, long span);
+
+// Staging plans (kv_stage.hip): a flush with the arguments of kvp_stage_run,
+// prepared without launching. stage_plan_launch launches it on its own;
+// stage_plan_runs returns its argument block when it is argument-encoded and
+// not empty (else null), for launches that carry it.
+void* stage_plan_create(void* stager, void* arena, long row_stride_bytes,
+                        const KvpRowCopy* copies, long n_copies, long* map_dev,
+                        long map_fill, const long* map_rows,
+                        const long* map_slots, long n_map);
+const void* stage_plan_runs(const void* plan);
+int stage_plan_launch(const void* plan, void* stream);
+void stage_plan_free(void* plan);
 
 }  // namespace kvp

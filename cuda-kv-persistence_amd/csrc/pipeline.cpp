@@ -19,7 +19,13 @@
 // frame (prefix reset to -1, then the staged rows), so after step 4 the
 // device map holds that map on the whole prefix (and -1 beyond it).
 // Nothing synchronises the host per frame: staging, map updates and
-// attention are ordered on the pipeline's stream.
+// attention are ordered on the pipeline's stream. kvp_pipeline_step runs
+// steps 1-5 for one frame in that order; kvp_pipeline_run plans frame f+1
+// before launching frame f and has frame f's attention launch carry frame
+// f+1's staging (as trailing workgroups of its split-combine launch, or as
+// the launch right after it), which saves one launch per frame. The staging
+// of frame f+1 still runs after frame f's attention has read the arena and
+// the map, so device results are those of frame-by-frame stepping.
 
 #include <algorithm>
 #include <cstring>
@@ -74,45 +80,22 @@ struct Pipeline {
 
 Pipeline* PL(void* p) { return static_cast<Pipeline*>(p); }
 
-int step_frame(Pipeline& p, int f, const char* q, const char* k, const char* v, char* out,
-               const float* scores_flat) {
-    if (f != p.next_frame) {
-        kvp::set_error("pipeline: frame %d stepped out of order (expected %d)", f, p.next_frame);
-        return 1;
-    }
+long window_first_frame(const Pipeline& p, int f) {
+    return (p.cross && p.window > 0 && f + 1 > p.window) ? f + 1 - p.window : 0;
+}
+
+// Steps 1-4 of a gated frame: selection, streaming release, staging and the
+// KVMap difference, prepared as one staging plan (*plan; launched by the
+// caller, not here). Host bookkeeping only.
+int plan_frame(Pipeline& p, int f, const char* k, const char* v, const float* scores_flat, void** plan) {
+    *plan = nullptr;
     const long T = p.T;
-    const long D = p.D;
-    const long row_bytes = D * p.elem;
-    const long frame_bytes = T * row_bytes;
-    const bool need_data = !p.plan_only;
-    if (need_data && (!q || !k || !v || !out)) {
-        kvp::set_error("pipeline: null q/k/v/out");
-        return 1;
-    }
-
-    long kb_frame = 0;
-    if (p.cross && p.window > 0 && f + 1 > p.window) kb_frame = f + 1 - p.window;
-
-    if (!p.persist) {
-        p.count = 0;
-        p.staged_tiles = 0;
-        p.copy_rows = 0;
-        p.next_frame = (f + 1 == p.frames) ? 0 : f + 1;
-        if (p.plan_only) return 0;
-        // Same per-frame launch structure as the gated policies.
-        if (p.cross)
-            return kvp::launch_attention(p.dtype, q + f * frame_bytes, k, v, nullptr, nullptr,
-                                         out + f * frame_bytes, p.T, p.D, p.heads, 1, 0, 0, 0,
-                                         kb_frame * T, (long)(f + 1) * T, p.stream);
-        return kvp::launch_attention(p.dtype, q + f * frame_bytes, k + f * frame_bytes,
-                                     v + f * frame_bytes, nullptr, nullptr,
-                                     out + f * frame_bytes, p.T, p.D, p.heads, 1, 0, 0, 0, 0, T,
-                                     p.stream);
-    }
+    const long row_bytes = (long)p.D * p.elem;
     if (!scores_flat) {
         kvp::set_error("pipeline: policy %s needs motion scores", p.policy->name());
         return 1;
     }
+    const long kb_frame = window_first_frame(p, f);
 
     KVTileManager& mgr = *p.mgr;
     if (f == 0) {
@@ -192,7 +175,7 @@ int step_frame(Pipeline& p, int f, const char* q, const char* k, const char* v, 
         if (all) ++p.staged_tiles;
     }
 
-    // 4. one flush: row copies + changed map entries in one launch
+    // 4. row copies + changed map entries, as one staging plan
     if (!p.plan_only) {
         ++p.step_id;
         p.upd_rows.clear();
@@ -214,8 +197,8 @@ int step_frame(Pipeline& p, int f, const char* q, const char* k, const char* v, 
             }
         }
         p.dev_rows = p.map_rows;
-        if (!mgr.flush_with_map(p.d_map, 0, p.upd_rows.data(), p.upd_vals.data(),
-                                p.upd_rows.size())) {
+        if (!mgr.flush_plan(plan, p.d_map, 0, p.upd_rows.data(), p.upd_vals.data(),
+                            p.upd_rows.size())) {
             return 1;
         }
     }
@@ -223,28 +206,100 @@ int step_frame(Pipeline& p, int f, const char* q, const char* k, const char* v, 
         (void)mgr.streaming_apply_window();
     else
         (void)mgr.arena_apply_window();
+    return 0;
+}
 
-    // 5. attention
-    int rc = 0;
-    if (!p.plan_only) {
-        const void* arena = mgr.arena_device_ptr();
-        if (p.cross)
-            rc = kvp::launch_attention(p.dtype, q + f * frame_bytes, k, v, arena, p.d_map,
-                                       out + f * frame_bytes, p.T, p.D, p.heads, 1, 0, 0, 0,
-                                       kb_frame * T, (long)(f + 1) * T, p.stream);
-        else
-            rc = kvp::launch_attention(p.dtype, q + f * frame_bytes, k + f * frame_bytes,
-                                       v + f * frame_bytes, arena, p.d_map + (long)f * T,
-                                       out + f * frame_bytes, p.T, p.D, p.heads, 1, 0, 0, 0, 0,
-                                       T, p.stream);
-    }
+// Step 5: the frame's attention launch, followed on the stream by the
+// staging plan `follow` (may be null).
+int launch_frame(Pipeline& p, int f, const char* q, const char* k, const char* v, char* out,
+                 const void* follow) {
+    const long T = p.T;
+    const long frame_bytes = T * (long)p.D * p.elem;
+    const long kb_frame = window_first_frame(p, f);
+    const void* arena = p.persist ? p.mgr->arena_device_ptr() : nullptr;
+    const long* map = p.persist ? p.d_map : nullptr;
+    if (p.cross)
+        return kvp::launch_attention(p.dtype, q + f * frame_bytes, k, v, arena, map,
+                                     out + f * frame_bytes, p.T, p.D, p.heads, 1, 0, 0, 0,
+                                     kb_frame * T, (long)(f + 1) * T, p.stream, follow);
+    return kvp::launch_attention(p.dtype, q + f * frame_bytes, k + f * frame_bytes,
+                                 v + f * frame_bytes, arena, map ? map + (long)f * T : nullptr,
+                                 out + f * frame_bytes, p.T, p.D, p.heads, 1, 0, 0, 0, 0, T, p.stream,
+                                 follow);
+}
 
+// Step 6: end of the frame's step in the manager.
+void finish_frame(Pipeline& p, int f) {
     if (p.streaming)
         p.prev_selected = p.selected;
     else
-        mgr.arena_end_step();
-    if (p.streaming && f + 1 == p.frames) mgr.streaming_end();
+        p.mgr->arena_end_step();
+    if (p.streaming && f + 1 == p.frames) p.mgr->streaming_end();
+}
+
+bool check_data(const Pipeline& p, const char* q, const char* k, const char* v, const char* out) {
+    if (!p.plan_only && (!q || !k || !v || !out)) {
+        kvp::set_error("pipeline: null q/k/v/out");
+        return false;
+    }
+    return true;
+}
+
+// One frame, in order: plan, staging launch, attention launch, step end.
+int step_frame(Pipeline& p, int f, const char* q, const char* k, const char* v, char* out,
+               const float* scores_flat) {
+    if (f != p.next_frame) {
+        kvp::set_error("pipeline: frame %d stepped out of order (expected %d)", f, p.next_frame);
+        return 1;
+    }
+    if (!check_data(p, q, k, v, out)) return 1;
+    if (!p.persist) {
+        p.count = 0;
+        p.staged_tiles = 0;
+        p.copy_rows = 0;
+        p.next_frame = (f + 1 == p.frames) ? 0 : f + 1;
+        if (p.plan_only) return 0;
+        return launch_frame(p, f, q, k, v, out, nullptr);
+    }
+    void* plan = nullptr;
+    int rc = plan_frame(p, f, k, v, scores_flat, &plan);
+    if (rc == 0 && plan) rc = kvp::stage_plan_launch(plan, p.stream);
+    kvp::stage_plan_free(plan);
+    if (rc == 0 && !p.plan_only) rc = launch_frame(p, f, q, k, v, out, nullptr);
+    if (rc) return rc;
+    finish_frame(p, f);
     p.next_frame = (f + 1 == p.frames) ? 0 : f + 1;
+    return 0;
+}
+
+// All frames, the staging of frame f+1 carried by frame f's attention
+// launch: frame f+1 is planned (host bookkeeping) before frame f's launch,
+// and its copies and map updates run right after frame f's attention on the
+// stream, as trailing workgroups of its split-combine launch when there is
+// one. Device results equal frame-by-frame stepping.
+int run_frames(Pipeline& p, const char* q, const char* k, const char* v, char* out,
+               const float* scores_flat) {
+    p.next_frame = 0;
+    if (!p.persist || p.plan_only) {
+        for (int f = 0; f < p.frames; ++f) {
+            const int rc = step_frame(p, f, q, k, v, out, scores_flat);
+            if (rc) return rc;
+        }
+        return 0;
+    }
+    if (!check_data(p, q, k, v, out)) return 1;
+    void* plan = nullptr;
+    int rc = plan_frame(p, 0, k, v, scores_flat, &plan);
+    if (rc == 0 && plan) rc = kvp::stage_plan_launch(plan, p.stream);
+    kvp::stage_plan_free(plan);
+    for (int f = 0; rc == 0 && f < p.frames; ++f) {
+        finish_frame(p, f);
+        void* next = nullptr;
+        if (f + 1 < p.frames) rc = plan_frame(p, f + 1, k, v, scores_flat, &next);
+        if (rc == 0) rc = launch_frame(p, f, q, k, v, out, next);
+        kvp::stage_plan_free(next);
+    }
+    p.next_frame = 0;
     return rc;
 }
 
@@ -336,13 +391,8 @@ int kvp_pipeline_step(void* p, int f, const void* q, const void* k, const void* 
 
 int kvp_pipeline_run(void* p, const void* q, const void* k, const void* v, void* out,
                      const float* scores_flat) {
-    Pipeline& pl = *PL(p);
-    pl.next_frame = 0;
-    for (int f = 0; f < pl.frames; ++f) {
-        const int rc = kvp_pipeline_step(p, f, q, k, v, out, scores_flat);
-        if (rc) return rc;
-    }
-    return 0;
+    return run_frames(*PL(p), static_cast<const char*>(q), static_cast<const char*>(k),
+                      static_cast<const char*>(v), static_cast<char*>(out), scores_flat);
 }
 
 int kvp_pipeline_selected(void* p, long* ids, int cap) {

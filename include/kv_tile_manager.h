@@ -104,6 +104,12 @@ public:
     // builds the map on the device instead of uploading a host copy.
     bool flush_with_map(long* map_dev, long map_fill, const long* map_rows,
                         const long* map_slots, size_t n_map) const;
+    // Same flush, prepared but not launched: *plan receives a staging plan
+    // (launched later by the library, e.g. together with the attention
+    // launch that precedes it; nullptr when there is nothing to do or the
+    // manager is plan-only). The pending copies are handed over at once.
+    bool flush_plan(void** plan, long* map_dev, long map_fill, const long* map_rows,
+                    const long* map_slots, size_t n_map) const;
 
 private:
     bool record_copy(long dst_row, const void* k_dev, size_t k_bytes,
