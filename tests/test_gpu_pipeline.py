@@ -162,3 +162,43 @@ def test_c5_shape_single_frame_pair_bf16():
     q, k, v = qkv[0], qkv[1], qkv[2]
     want = at.attention_keys(q[T:T + 128], k[:2 * T], v[:2 * T], HEADS)
     assert float((base.float().cpu()[T:T + 128] - want).abs().max()) <= 2e-2
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("streaming", [False, True])
+def test_run_carried_staging_equals_stepping(dtype, streaming):
+    """kvp_pipeline_run plans frame f+1 before launching frame f and lets the
+    attention launch of frame f carry frame f+1's staging. Outputs must equal
+    frame-by-frame stepping bitwise, and after the run the device KVMap and
+    the arena must hold the last frame's state of the oracle driver."""
+    cfg = workloads.CONFIGS["c3"]
+    frames, T = 4, cfg.tokens
+    qkv = _device_inputs(frames, T, dtype, seed=9)
+    _, _, _, qd, kd, vd = qkv
+    scores = workloads.motion_for(cfg, 1)[:frames]
+    set_aside = cfg.set_aside if dtype == torch.bfloat16 else 2 * cfg.set_aside
+    elem = 4 if dtype == torch.float32 else 2
+    stepped = _run_pipeline("motion", cross=True, streaming=streaming, frames=frames, T=T,
+                            dtype=dtype, set_aside=set_aside, scores=scores, qkv=qkv)
+    d = 0 if dtype == torch.float32 else 1
+    pl = FramePipeline("motion", cross=True, streaming=streaming, frames=frames, T=T, D=D,
+                       heads=HEADS, tile_tokens=16, set_aside_bytes=set_aside, dtype=d)
+    pl.set_scores(scores)
+    out = torch.empty_like(qd)
+    for _ in range(2):  # a second pass reuses the pipeline's device state
+        pl.run(qd, kd, vd, out)
+        torch.cuda.synchronize()
+        assert torch.equal(out, stepped), streaming
+    plan = mm.plan_frames("motion", cross=True, streaming=streaming, frames=frames, T=T, D=D,
+                          tile_tokens=16, set_aside=set_aside, elem=elem, scores_flat=scores)
+    dmap = _device_map(pl, frames * T)
+    np.testing.assert_array_equal(dmap, plan[frames - 1]["map"])
+    rows = np.nonzero(dmap >= 0)[0]
+    assert rows.size > 0
+    arena = _arena_rows(pl, set_aside // (2 * D * elem), dtype)
+    kflat, vflat = kd.view(frames * T, D), vd.view(frames * T, D)
+    slots = torch.from_numpy(dmap[rows]).to(DEV)
+    ridx = torch.from_numpy(rows).to(DEV)
+    assert torch.equal(arena[slots, :D], kflat[ridx])
+    assert torch.equal(arena[slots, D:], vflat[ridx])
+    pl.close()
