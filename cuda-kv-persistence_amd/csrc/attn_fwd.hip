@@ -309,6 +309,12 @@ __device__ __forceinline__ void lgkm_wait2_keep2(u32x4& a, u32x4& b) {
     asm volatile("s_waitcnt lgkmcnt(2)" : "+v"(a), "+v"(b)::"memory");
 }
 
+// Waits until at most N LDS reads are outstanding.
+template <int N>
+__device__ __forceinline__ void lgkm_wait_tr_n(u32x2& a, u32x2& b, u32x2& c, u32x2& d) {
+    asm volatile("s_waitcnt lgkmcnt(%4)" : "+v"(a), "+v"(b), "+v"(c), "+v"(d) : "n"(N) : "memory");
+}
+
 __device__ __forceinline__ void lgkm_wait_tr(u32x2& a, u32x2& b, u32x2& c, u32x2& d) {
     asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(a), "+v"(b), "+v"(c), "+v"(d)::"memory");
 }
@@ -380,24 +386,18 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_bf16_kernel(AttnArgs a) 
 
     // KVMap entries of a tile are copied into LDS two tiles ahead (one
     // 4-byte copy per lane: wave w takes the tile's rows 16w.. as 32 words;
-    // lanes past the tile's end read zeros), before the copies of the tile in
-    // between. Right before the tile's own K/V copies are issued they are
-    // decoded into arena byte offsets; memory counters retire in issue order,
-    // so that decode waits on the map copy alone while the copies of the tile
-    // in between stay in flight. Any negative entry, or one of 2^31 or more,
+    // lanes past the tile's end read zeros). Right before the tile's own K/V
+    // copies are issued they are decoded into arena byte offsets; by then
+    // the map copy has landed (the loop waits for all of a wave's copies at
+    // the top of each iteration). Any negative entry, or one of 2^31 or more,
     // reads the original K/V row (offset ~0u).
     const unsigned m_wave = (unsigned)(uintptr_t)m_lds + 256u * wave;
     unsigned mdec[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) mdec[i] = ~0u;
-    // map copy of tile `t` outstanding behind exactly `behind` later vector
-    // memory operations
-    auto decode_map = [&](int t, bool behind8) {
+    auto decode_map = [&](int t) {
         if (!map) return;
-        if (behind8)
-            wait_vm<8>();
-        else
-            wait_vm<0>();
+        wait_vm<0>();
         const unsigned ad = m_wave + 1024u * (unsigned)(t & 1) + 8u * (unsigned)(lane >> 4);
         u32x2 m0 = lds_b64<0>(ad), m1 = lds_b64<32>(ad), m2 = lds_b64<64>(ad), m3 = lds_b64<96>(ad);
         lgkm_wait_tr(m0, m1, m2, m3);
@@ -417,42 +417,38 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_bf16_kernel(AttnArgs a) 
             (unsigned)__builtin_amdgcn_readfirstlane((int)m_wave) + 1024u * (unsigned)(t & 1));
         __builtin_amdgcn_raw_ptr_buffer_load_lds(mrs, md, 4, 128u * wave + 4u * lane, 0, 0, 0);
     };
-    auto issue_tile = [&](int t, unsigned char* kdst, unsigned char* vdst) {
+    // A tile's copies are set up by prep_tile (descriptors and LDS bases)
+    // and issued as 4 K/V pairs by copy_pair(i). Issued back to back, a
+    // wave's 8 copies (1 KiB each) kept it stalled on instruction issue for
+    // about a quarter of every tile on MI355X, while both workgroups of the
+    // CU pushed their 64 KiB through the load path at once; the main loop
+    // instead issues one pair after every second QK k-step of the tile being
+    // computed, so the copies trickle out between MFMAs.
+    __amdgpu_buffer_rsrc_t krs, vrs;
+    unsigned koff = 0, voff = 0;
+    auto prep_tile = [&](int t, unsigned char* kdst, unsigned char* vdst) {
         const long t0 = kbeg + (long)t * kBf16BlockKeys;
         const long left = kend - t0;
         const int nrec = (int)((left < kBf16BlockKeys ? left : kBf16BlockKeys) * (long)rb);
-        const __amdgpu_buffer_rsrc_t krs = __builtin_amdgcn_make_buffer_rsrc(
-            const_cast<unsigned char*>(Kb + t0 * (long)rb), (short)0, nrec, kBufFlags);
-        const __amdgpu_buffer_rsrc_t vrs = __builtin_amdgcn_make_buffer_rsrc(
-            const_cast<unsigned char*>(Vb + t0 * (long)rb), (short)0, nrec, kBufFlags);
-        const unsigned koff = (unsigned)__builtin_amdgcn_readfirstlane((int)(uintptr_t)kdst) + 4096u * wave;
-        const unsigned voff = (unsigned)__builtin_amdgcn_readfirstlane((int)(uintptr_t)vdst) + 4096u * wave;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            KVP_LDS void* kd = (KVP_LDS void*)(uintptr_t)(koff + 1024u * i);
-            KVP_LDS void* vd = (KVP_LDS void*)(uintptr_t)(voff + 1024u * i);
-            const unsigned row_off = lane_row + 4u * i * rb;
-            if (map && mdec[i] != ~0u) {
-                const unsigned ao = mdec[i];
-                __builtin_amdgcn_raw_ptr_buffer_load_lds(arena_rs, kd, 16, ao + kofs[i], 0, 0, 0);
-                __builtin_amdgcn_raw_ptr_buffer_load_lds(arena_rs, vd, 16, ao + rb + vofs, 0, 0, 0);
-            } else {
-                __builtin_amdgcn_raw_ptr_buffer_load_lds(krs, kd, 16, row_off + kofs[i], 0, 0, 0);
-                __builtin_amdgcn_raw_ptr_buffer_load_lds(vrs, vd, 16, row_off + vofs, 0, 0, 0);
-            }
-        }
+        krs = __builtin_amdgcn_make_buffer_rsrc(const_cast<unsigned char*>(Kb + t0 * (long)rb),
+                                                (short)0, nrec, kBufFlags);
+        vrs = __builtin_amdgcn_make_buffer_rsrc(const_cast<unsigned char*>(Vb + t0 * (long)rb),
+                                                (short)0, nrec, kBufFlags);
+        koff = (unsigned)__builtin_amdgcn_readfirstlane((int)(uintptr_t)kdst) + 4096u * wave;
+        voff = (unsigned)__builtin_amdgcn_readfirstlane((int)(uintptr_t)vdst) + 4096u * wave;
     };
-    // Waits until the copies of the tile about to be computed have landed.
-    // Issued after them: the map copy of the tile after next (when a map is
-    // read and that tile exists) and the 8 copies of the next tile; those
-    // stay in flight.
-    auto wait_current = [&](bool more, bool map_ahead) {
-        if (!more)
-            wait_vm<0>();
-        else if (map_ahead)
-            wait_vm<9>();
-        else
-            wait_vm<8>();
+    auto copy_pair = [&](int i) {
+        KVP_LDS void* kd = (KVP_LDS void*)(uintptr_t)(koff + 1024u * i);
+        KVP_LDS void* vd = (KVP_LDS void*)(uintptr_t)(voff + 1024u * i);
+        const unsigned row_off = lane_row + 4u * i * rb;
+        if (map && mdec[i] != ~0u) {
+            const unsigned ao = mdec[i];
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(arena_rs, kd, 16, ao + kofs[i], 0, 0, 0);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(arena_rs, vd, 16, ao + rb + vofs, 0, 0, 0);
+        } else {
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(krs, kd, 16, row_off + kofs[i], 0, 0, 0);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(vrs, vd, 16, row_off + vofs, 0, 0, 0);
+        }
     };
 
     f32x16 o[4];
@@ -473,7 +469,10 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_bf16_kernel(AttnArgs a) 
     const int vsub = 8 * (tr_r & 1);
     const unsigned vcl = (unsigned)(2 * (grp & 1) + (tr_r >> 1));  // chunk bits below 4*nb
 
-    auto compute_tile = [&](int t, const unsigned char* ks_lds, const unsigned char* vt_lds) {
+    // `between(ks)` runs after the MFMAs of QK k-step ks (the next tile's
+    // copies are issued there).
+    auto compute_tile = [&](int t, const unsigned char* ks_lds, const unsigned char* vt_lds,
+                            auto&& between) {
         const unsigned kbase = (unsigned)(uintptr_t)ks_lds + (unsigned)(lq * 256);
         f32x16 s0, s1;
 #pragma unroll
@@ -511,9 +510,36 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_bf16_kernel(AttnArgs a) 
                                                          qf[ks], s0, 0, 0, 0);
             s1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, kb[cur]),
                                                          qf[ks], s1, 0, 0, 0);
+            between(ks);
         }
 
         __builtin_amdgcn_s_setprio(0);
+
+        // O^T += V^T P^T reads V^T fragments with transposing LDS reads of
+        // rows 16g + 4hh + s and +8 (row offsets 16g*256 and 8*256 are
+        // immediates): 8 reads per 32-column block nb, in two groups of 4
+        // that feed 2 MFMAs each. Block 0 is read now, ahead of the softmax;
+        // each later group is read one block ahead of its MFMAs.
+        const unsigned vbase = (unsigned)(uintptr_t)vt_lds + (unsigned)((4 * hh + tr_s) * 256 + vsub);
+        auto vaddr = [&](int nb) { return vbase + ((((unsigned)(4 * nb) | vcl) ^ vs) << 4); };
+        u32x2 vr[2][8];
+        auto read_v = [&](u32x2* d, int nb, int half) {
+            const unsigned ad = vaddr(nb);
+            if (half == 0) {
+                d[0] = lds_tr16<0>(ad);
+                d[1] = lds_tr16<8 * 256>(ad);
+                d[2] = lds_tr16<16 * 256>(ad);
+                d[3] = lds_tr16<24 * 256>(ad);
+            } else {
+                d[4] = lds_tr16<32 * 256>(ad);
+                d[5] = lds_tr16<40 * 256>(ad);
+                d[6] = lds_tr16<48 * 256>(ad);
+                d[7] = lds_tr16<56 * 256>(ad);
+            }
+        };
+        read_v(vr[0], 0, 0);
+        read_v(vr[0], 0, 1);
+
         float s[32];
 #pragma unroll
         for (int v = 0; v < 16; ++v) {
@@ -522,11 +548,14 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_bf16_kernel(AttnArgs a) 
         }
         const long t0 = kbeg + (long)t * kBf16BlockKeys;
         if (t0 + kBf16BlockKeys > kend) {
-            const long lim = kend - t0;
+            // s[v] holds key kc(v) + 4*hh of the tile, kc(v) a compile-time
+            // constant: comparing kc(v) with lim - 4*hh keeps the per-lane
+            // key indices out of registers.
+            const int lim = (int)(kend - t0) - 4 * hh;
 #pragma unroll
             for (int v = 0; v < 32; ++v) {
-                const int key = 32 * (v >> 4) + 8 * ((v & 15) >> 2) + 4 * hh + (v & 3);
-                if (key >= lim) s[v] = -INFINITY;
+                const int kc = 32 * (v >> 4) + 8 * ((v & 15) >> 2) + (v & 3);
+                if (kc >= lim) s[v] = -INFINITY;
             }
         }
 
@@ -574,27 +603,29 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_bf16_kernel(AttnArgs a) 
         }
         l_run += tot;
 
-        // O^T += V^T P^T; transposed V reads of rows 16g + 4hh + s and +8
-        // (row offsets 16g*256 and 8*256 are immediates).
-        const unsigned vbase = (unsigned)(uintptr_t)vt_lds + (unsigned)((4 * hh + tr_s) * 256 + vsub);
+        // LDS reads complete in issue order, so lgkmcnt(4) waits for the
+        // older of the two groups in flight.
         __builtin_amdgcn_s_setprio(1);
 #pragma unroll
         for (int nb = 0; nb < 4; ++nb) {
-            const unsigned ad = vbase + ((((unsigned)(4 * nb) | vcl) ^ vs) << 4);
-            u32x2 v0 = lds_tr16<0>(ad), v1 = lds_tr16<8 * 256>(ad);
-            u32x2 v2 = lds_tr16<16 * 256>(ad), v3 = lds_tr16<24 * 256>(ad);
-            lgkm_wait_tr(v0, v1, v2, v3);
-            u32x2 w0 = lds_tr16<32 * 256>(ad), w1 = lds_tr16<40 * 256>(ad);
-            u32x2 w2 = lds_tr16<48 * 256>(ad), w3 = lds_tr16<56 * 256>(ad);
-            const u32x4 va0 = {v0[0], v0[1], v1[0], v1[1]};
-            const u32x4 va1 = {v2[0], v2[1], v3[0], v3[1]};
+            u32x2* cur = vr[nb & 1];
+            u32x2* nxt = vr[(nb + 1) & 1];
+            lgkm_wait_tr_n<4>(cur[0], cur[1], cur[2], cur[3]);
+            if (nb < 3) read_v(nxt, nb + 1, 0);
+            const u32x4 va0 = {cur[0][0], cur[0][1], cur[1][0], cur[1][1]};
+            const u32x4 va1 = {cur[2][0], cur[2][1], cur[3][0], cur[3][1]};
             o[nb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, va0), pb[0],
                                                             o[nb], 0, 0, 0);
             o[nb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, va1), pb[1],
                                                             o[nb], 0, 0, 0);
-            lgkm_wait_tr(w0, w1, w2, w3);
-            const u32x4 va2 = {w0[0], w0[1], w1[0], w1[1]};
-            const u32x4 va3 = {w2[0], w2[1], w3[0], w3[1]};
+            if (nb < 3) {
+                lgkm_wait_tr_n<4>(cur[4], cur[5], cur[6], cur[7]);
+                read_v(nxt, nb + 1, 1);
+            } else {
+                lgkm_wait_tr_n<0>(cur[4], cur[5], cur[6], cur[7]);
+            }
+            const u32x4 va2 = {cur[4][0], cur[4][1], cur[5][0], cur[5][1]};
+            const u32x4 va3 = {cur[6][0], cur[6][1], cur[7][0], cur[7][1]};
             o[nb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, va2), pb[2],
                                                             o[nb], 0, 0, 0);
             o[nb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, va3), pb[3],
@@ -605,25 +636,33 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_bf16_kernel(AttnArgs a) 
 
     if (ntiles > 0) {
         load_map(0);
-        decode_map(0, false);
+        decode_map(0);
         if (ntiles > 1) load_map(1);
-        issue_tile(0, k_lds0, v_lds0);
+        prep_tile(0, k_lds0, v_lds0);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) copy_pair(i);
     }
     for (int t = 0; t < ntiles; ++t) {
-        // tile t lives in stage t & 1; tile t+1 streams into the other stage
+        // tile t lives in stage t & 1; tile t+1 streams into the other stage,
+        // which every wave finished reading before the barrier that closed
+        // the previous iteration
         unsigned char* kcur = (t & 1) ? k_lds1 : k_lds0;
         unsigned char* vcur = (t & 1) ? v_lds1 : v_lds0;
         unsigned char* knext = (t & 1) ? k_lds0 : k_lds1;
         unsigned char* vnext = (t & 1) ? v_lds0 : v_lds1;
-        const bool map_ahead = map && t + 2 < ntiles;
-        if (t + 1 < ntiles) {
-            decode_map(t + 1, true);
-            if (map_ahead) load_map(t + 2);
-            issue_tile(t + 1, knext, vnext);
-        }
-        wait_current(t + 1 < ntiles, map_ahead);
+        const bool more = t + 1 < ntiles;
+        // each wave's copies of tile t (and map copies) have landed, then
+        // the barrier publishes the whole tile
+        wait_vm<0>();
         wg_barrier();
-        compute_tile(t, kcur, vcur);
+        if (more) {
+            decode_map(t + 1);
+            if (map && t + 2 < ntiles) load_map(t + 2);
+            prep_tile(t + 1, knext, vnext);
+        }
+        compute_tile(t, kcur, vcur, [&](int ks) {
+            if (more && (ks & 1) == 0) copy_pair(ks >> 1);
+        });
         wg_barrier();
     }
 
