@@ -319,7 +319,9 @@ __device__ __forceinline__ void lgkm_wait_tr(u32x2& a, u32x2& b, u32x2& c, u32x2
     asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(a), "+v"(b), "+v"(c), "+v"(d)::"memory");
 }
 
-template <typename OutT>
+// kMap: the launch reads a KVMap (a.kvmap != null); the map-free variant has
+// no per-row source selection in its copy path.
+template <typename OutT, bool kMap>
 __global__ __launch_bounds__(kThreads, 2) void attn_fwd_bf16_kernel(AttnArgs a) {
     __shared__ __attribute__((aligned(1024))) unsigned char k_lds0[kBf16TileBytes];
     __shared__ __attribute__((aligned(1024))) unsigned char v_lds0[kBf16TileBytes];
@@ -331,7 +333,7 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_bf16_kernel(AttnArgs a) 
 
     const WgCoord c = decode_wg(a);
     const int tid = threadIdx.x;
-    const int wave = tid >> 6;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int lane = tid & 63;
     const int lq = lane & 31;
     const int hh = lane >> 5;
@@ -345,7 +347,7 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_bf16_kernel(AttnArgs a) 
     const unsigned char* Kb = reinterpret_cast<const unsigned char*>(a.k) + 2L * c.frame * a.kv_fstride;
     const unsigned char* Vb = reinterpret_cast<const unsigned char*>(a.v) + 2L * c.frame * a.kv_fstride;
     const unsigned char* Ab = reinterpret_cast<const unsigned char*>(a.arena);
-    const long* map = a.kvmap ? a.kvmap + (long)c.frame * a.map_fstride : nullptr;
+    const long* map = kMap ? a.kvmap + (long)c.frame * a.map_fstride : nullptr;
     const long row_bytes = 2L * a.D;
     const long hoff_b = 2L * c.head * kHeadDim;
 
@@ -396,7 +398,7 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_bf16_kernel(AttnArgs a) 
 #pragma unroll
     for (int i = 0; i < 4; ++i) mdec[i] = ~0u;
     auto decode_map = [&](int t) {
-        if (!map) return;
+        if constexpr (!kMap) return;
         wait_vm<0>();
         const unsigned ad = m_wave + 1024u * (unsigned)(t & 1) + 8u * (unsigned)(lane >> 4);
         u32x2 m0 = lds_b64<0>(ad), m1 = lds_b64<32>(ad), m2 = lds_b64<64>(ad), m3 = lds_b64<96>(ad);
@@ -407,7 +409,7 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_bf16_kernel(AttnArgs a) 
             mdec[i] = (mw[i][1] == 0u && (int)mw[i][0] >= 0) ? 2u * mw[i][0] * rb : ~0u;
     };
     auto load_map = [&](int t) {
-        if (!map) return;
+        if constexpr (!kMap) return;
         const long t0 = kbeg + (long)t * kBf16BlockKeys;
         const long left = kend - t0;
         const int nrec = (int)((left < kBf16BlockKeys ? left : kBf16BlockKeys) * 8);
@@ -429,7 +431,9 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_bf16_kernel(AttnArgs a) 
     auto prep_tile = [&](int t, unsigned char* kdst, unsigned char* vdst) {
         const long t0 = kbeg + (long)t * kBf16BlockKeys;
         const long left = kend - t0;
-        const int nrec = (int)((left < kBf16BlockKeys ? left : kBf16BlockKeys) * (long)rb);
+        // tiles at or past the end (the loop's trailing copies) cover no rows
+        const long rows = left <= 0 ? 0 : (left < kBf16BlockKeys ? left : kBf16BlockKeys);
+        const int nrec = (int)(rows * (long)rb);
         krs = __builtin_amdgcn_make_buffer_rsrc(const_cast<unsigned char*>(Kb + t0 * (long)rb),
                                                 (short)0, nrec, kBufFlags);
         vrs = __builtin_amdgcn_make_buffer_rsrc(const_cast<unsigned char*>(Vb + t0 * (long)rb),
@@ -441,7 +445,7 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_bf16_kernel(AttnArgs a) 
         KVP_LDS void* kd = (KVP_LDS void*)(uintptr_t)(koff + 1024u * i);
         KVP_LDS void* vd = (KVP_LDS void*)(uintptr_t)(voff + 1024u * i);
         const unsigned row_off = lane_row + 4u * i * rb;
-        if (map && mdec[i] != ~0u) {
+        if (kMap && mdec[i] != ~0u) {
             const unsigned ao = mdec[i];
             __builtin_amdgcn_raw_ptr_buffer_load_lds(arena_rs, kd, 16, ao + kofs[i], 0, 0, 0);
             __builtin_amdgcn_raw_ptr_buffer_load_lds(arena_rs, vd, 16, ao + rb + vofs, 0, 0, 0);
@@ -563,6 +567,11 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_bf16_kernel(AttnArgs a) 
         // overflows the bound (first tile, where the running max is -inf, or
         // scores that grew far beyond it) take the slow path: raise the max
         // to the tile max, rescale O and l, and exponentiate again.
+        // The row sum adds the fp32 exponentials with plain VALU adds: the
+        // packed bf16 dot instruction would sum the rounded P exactly, but on
+        // gfx950 it does not issue while the other wave of the SIMD streams
+        // MFMAs (measured), which stalls this softmax behind the other
+        // wave's matrix work.
         bf16x8 pb[4];
         auto exp_tile = [&](float mref) {
             float rs = 0.f;
@@ -570,13 +579,11 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_bf16_kernel(AttnArgs a) 
             for (int g = 0; g < 4; ++g) {
 #pragma unroll
                 for (int i = 0; i < 8; i += 2) {
-                    bf16x2 pr;
-                    pr[0] = (__bf16)fast_exp2(fmaf(s[8 * g + i], cl2, -mref));
-                    pr[1] = (__bf16)fast_exp2(fmaf(s[8 * g + i + 1], cl2, -mref));
-                    pb[g][i] = pr[0];
-                    pb[g][i + 1] = pr[1];
-                    const bf16x2 one = {(__bf16)1.0f, (__bf16)1.0f};
-                    rs = __builtin_amdgcn_fdot2_f32_bf16(pr, one, rs, false);
+                    const float e0 = fast_exp2(fmaf(s[8 * g + i], cl2, -mref));
+                    const float e1 = fast_exp2(fmaf(s[8 * g + i + 1], cl2, -mref));
+                    pb[g][i] = (__bf16)e0;
+                    pb[g][i + 1] = (__bf16)e1;
+                    rs += e0 + e1;
                 }
             }
             float rlo, rhi;
@@ -655,16 +662,25 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_bf16_kernel(AttnArgs a) 
         // the barrier publishes the whole tile
         wait_vm<0>();
         wg_barrier();
+        // The copies for tile t+1 are issued unconditionally, so the QK
+        // k-steps they sit between stay one basic block: past the last tile
+        // the descriptors cover no rows (every row reads as zeros) and no
+        // KVMap words are decoded (every row takes the original K/V path).
         if (more) {
             decode_map(t + 1);
-            if (map && t + 2 < ntiles) load_map(t + 2);
-            prep_tile(t + 1, knext, vnext);
+            if (kMap && t + 2 < ntiles) load_map(t + 2);
+        } else if (kMap) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) mdec[i] = ~0u;
         }
+        prep_tile(t + 1, knext, vnext);
         compute_tile(t, kcur, vcur, [&](int ks) {
-            if (more && (ks & 1) == 0) copy_pair(ks >> 1);
+            if ((ks & 1) == 0) copy_pair(ks >> 1);
         });
         wg_barrier();
     }
+    // the trailing copies land before the workgroup's LDS is released
+    wait_vm<0>();
 
     store_rows<OutT>(a, c, q, hh, o, m_run, l_run);
 }
@@ -939,7 +955,7 @@ DeviceInfo device_info(int dev) {
         if (hipGetDeviceProperties(&prop, dev) == hipSuccess) di.cus = prop.multiProcessorCount;
         int nb = 0;
         if (hipOccupancyMaxActiveBlocksPerMultiprocessor(
-                &nb, attn_fwd_bf16_kernel<__bf16>, kThreads, 0) == hipSuccess && nb > 0)
+                &nb, attn_fwd_bf16_kernel<__bf16, true>, kThreads, 0) == hipSuccess && nb > 0)
             di.wg_per_cu_bf16 = nb;
         nb = 0;
         if (hipOccupancyMaxActiveBlocksPerMultiprocessor(
@@ -1115,7 +1131,12 @@ int launch_attention(int dtype, const void* q, const void* k, const void* v, con
     }
     hipStream_t st = static_cast<hipStream_t>(stream);
     if (dtype == 1) {
-        hipLaunchKernelGGL(attn_fwd_bf16_kernel<__bf16>, dim3((unsigned)p.grid), dim3(kThreads), 0, st, a);
+        if (a.kvmap)
+            hipLaunchKernelGGL((attn_fwd_bf16_kernel<__bf16, true>), dim3((unsigned)p.grid),
+                               dim3(kThreads), 0, st, a);
+        else
+            hipLaunchKernelGGL((attn_fwd_bf16_kernel<__bf16, false>), dim3((unsigned)p.grid),
+                               dim3(kThreads), 0, st, a);
     } else {
         hipLaunchKernelGGL(attn_fwd_f32_kernel, dim3((unsigned)p.grid), dim3(kThreads), 0, st, a);
     }
