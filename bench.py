@@ -172,8 +172,36 @@ def main():
     ms_step, wall_step = timed(main_pl, args.steps)
     log(f"policy {args.policy}: {ms_step:.3f} ms/step")
 
-    # --- per-policy pipeline timing and bitwise gate ---------------------------------
+    # --- attention kernel alone: HIP events around each frame's launch ---------------
+    # One launch per (layer, frame) with the policy's own arena and KVMap as the
+    # pipeline left them after its last step (none: no map, the map-free kernel
+    # instantiation), so each policy's figure times the kernel its pipeline runs.
+    # The events are recorded on the stream the launches go to.
+    stream = torch.cuda.current_stream().cuda_stream
+
+    def attn_pass(arena_ptr, map_ptr):
+        api.set_stream(stream)
+        evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+               for _ in range(layers * F)]
+        for rep in range(2):  # first pass warms, second is measured
+            i = 0
+            for layer in range(layers):
+                for f in range(F):
+                    a, b = evs[i]
+                    a.record()
+                    api.attn_forward_single_frame_bf16(qs[layer][f * T:(f + 1) * T], ks[layer],
+                                                       vs[layer], arena_ptr, map_ptr,
+                                                       outs[layer][f * T:(f + 1) * T], T, D, H,
+                                                       1, f)
+                    b.record()
+                    i += 1
+            torch.cuda.synchronize()
+        api.set_stream(None)
+        return sum(a.elapsed_time(b) for a, b in evs)
+
+    # --- per-policy pipeline timing, bitwise gate, attention-only pass -----------------
     policies = {}
+    attn_ms_by_policy = {}
     ref_out = None
     for pol in ("none", "recency", "motion"):
         pl = main_pl if pol == args.policy else make(pol)
@@ -184,37 +212,23 @@ def main():
             ref_out = o0
         policies[pol] = {"pipeline_ms_per_frame": round(t / F, 4),
                          "bitwise_equal_to_none": bool(torch.equal(o0, ref_out))}
+        arena_ptr, map_ptr = (pl.arena_ptr() or None), (pl.device_map_ptr() or None)
+        ms = attn_pass(arena_ptr if map_ptr else None, map_ptr if arena_ptr else None)
+        attn_ms_by_policy[pol] = ms
+        policies[pol]["attn_kernel_ms_per_frame"] = round(ms / F, 4)
+        policies[pol]["attn_kernel_reads_kvmap"] = bool(arena_ptr and map_ptr)
         if pl is not main_pl:
             pl.close()
-        log(f"policy {pol}: {t / F:.4f} ms/frame")
+        log(f"policy {pol}: {t / F:.4f} ms/frame, attention alone {ms / F:.4f} ms/frame")
 
-    # --- attention kernel roofline: HIP events around each frame's launch ------------
-    stream = torch.cuda.current_stream().cuda_stream
-    api.set_stream(stream)
+    # --- attention kernel roofline: the headline policy's attention-only pass --------
     fl_layer = cfg.flops_per_layer()
-    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-           for _ in range(layers * F)]
-    for rep in range(2):  # first pass warms, second is measured
-        i = 0
-        for layer in range(layers):
-            for f in range(F):
-                a, b = evs[i]
-                a.record()
-                api.attn_forward_single_frame_bf16(qs[layer][f * T:(f + 1) * T], ks[layer],
-                                                   vs[layer], None, None,
-                                                   outs[layer][f * T:(f + 1) * T], T, D, H, 1, f)
-                b.record()
-                i += 1
-        torch.cuda.synchronize()
-    api.set_stream(None)
-    attn_ms = sum(a.elapsed_time(b) for a, b in evs)
+    attn_ms = attn_ms_by_policy[args.policy]
     launches = layers * F
     flops_total = fl_layer * layers
     achieved = flops_total / (attn_ms * 1e-3) / 1e12
-    per_frame_attn = attn_ms / F
-    for pol in policies:
-        policies[pol]["attn_kernel_ms_per_frame"] = round(per_frame_attn, 4)
-    log(f"attention kernels: {attn_ms:.3f} ms over {launches} launches, {achieved:.1f} TFLOP/s")
+    log(f"attention kernels ({args.policy}): {attn_ms:.3f} ms over {launches} launches, "
+        f"{achieved:.1f} TFLOP/s")
 
     # Fabric bytes come from rocprofv3 FETCH_SIZE / WRITE_SIZE runs of this same
     # workload (bench.py --profile-policy P), scaled by a copy-kernel calibration
@@ -263,7 +277,9 @@ def main():
         },
         "roofline": {
             "bound": "mfma",
-            "kernel": "attn_fwd_bf16_kernel (+ split combine)",
+            "kernel": ("attn_fwd_bf16_kernel, KVMap instantiation (+ split combine)"
+                       if policies[args.policy]["attn_kernel_reads_kvmap"]
+                       else "attn_fwd_bf16_kernel, map-free instantiation (+ split combine)"),
             "achieved": round(achieved, 2),
             "peak": BF16_PEAK_TFLOPS,
             "unit": "TFLOP/s",
