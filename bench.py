@@ -238,7 +238,8 @@ def main():
     if tfile.exists():
         try:
             tj = json.loads(tfile.read_text())
-            traffic = tj.get("hbm_bytes_per_launch")
+            traffic = tj.get("policies", {}).get(args.policy, {}).get(
+                "attn_hbm_bytes_per_launch", tj.get("hbm_bytes_per_launch"))
             for pol, rec in tj.get("policies", {}).items():
                 if pol in policies:
                     policies[pol]["attn_read_bytes_per_frame"] = rec.get("attn_read_bytes_per_frame")
