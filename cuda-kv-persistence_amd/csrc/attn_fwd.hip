@@ -391,9 +391,12 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_bf16_kernel(AttnArgs a) 
     // lanes past the tile's end read zeros). Right before the tile's own K/V
     // copies are issued they are decoded into arena byte offsets; by then
     // the map copy has landed (the loop waits for all of a wave's copies at
-    // the top of each iteration). Any negative entry, or one of 2^31 or more,
-    // reads the original K/V row (offset ~0u).
+    // the top of each iteration). Arena rows are addressed with 32-bit byte
+    // offsets from the arena base: an entry m is used when its row ends
+    // within 4 GiB of that base (2*(m+1)*row_bytes <= 2^32); any negative
+    // entry, or one beyond that, reads the original K/V row (offset ~0u).
     const unsigned m_wave = (unsigned)(uintptr_t)m_lds + 256u * wave;
+    const unsigned max_arena_row = 0x80000000u / rb - 1u;
     unsigned mdec[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) mdec[i] = ~0u;
@@ -406,7 +409,7 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_bf16_kernel(AttnArgs a) 
         const u32x2 mw[4] = {m0, m1, m2, m3};
 #pragma unroll
         for (int i = 0; i < 4; ++i)
-            mdec[i] = (mw[i][1] == 0u && (int)mw[i][0] >= 0) ? 2u * mw[i][0] * rb : ~0u;
+            mdec[i] = (mw[i][1] == 0u && mw[i][0] <= max_arena_row) ? 2u * mw[i][0] * rb : ~0u;
     };
     auto load_map = [&](int t) {
         if constexpr (!kMap) return;

@@ -15,7 +15,10 @@
  *   - Layout: token-major [rows, D], D = heads * 128, element (t, h, d) at
  *     t*D + h*128 + d. Arena row = [K row (D) | V row (D)], stride 2*D
  *     elements. KVMap[j] >= 0 -> key row j lives at arena row KVMap[j];
- *     KVMap[j] < 0 -> read the original K/V row j.
+ *     KVMap[j] < 0 -> read the original K/V row j. The bf16 kernels address
+ *     the arena with 32-bit byte offsets: an entry m counts only while
+ *     2*(m+1)*row_bytes <= 2^32 (its row lies in the arena's first 4 GiB);
+ *     a larger entry reads the original row as a negative one does.
  */
 
 #include <stddef.h>

@@ -107,6 +107,48 @@ def test_kvmap_indirection_is_bitwise_invisible(dtype, mode):
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_kvmap_with_key_splits_is_bitwise_invisible(dtype):
+    """Cross-frame shape that splits the key range (several tiles per split, a
+    partial last tile): the KVMap launch equals the map-free launch bit for bit,
+    and both match the oracle."""
+    frames, T, heads = 2, 1560, 12
+    d = 1 if dtype == torch.bfloat16 else 0
+    assert api.attn_splits(d, T, heads, 1, frames * T) > 1
+    q, k, v = _inputs(frames, T, heads, seed=13, dtype=dtype)
+    base = _run(dtype, q, k, v, frames, T, heads, "cross")
+    rng = np.random.default_rng(14)
+    arena, kvmap = _random_arena(k.to(dtype), v.to(dtype), rng, frac=0.25)
+    got = _run(dtype, q, k, v, frames, T, heads, "cross", arena=arena.to(DEV).contiguous(),
+               kvmap=kvmap.to(DEV))
+    assert torch.equal(got, base)
+    _check(base, at.attention_frames(q, k, v, frames, T, heads, "cross"), dtype)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_kvmap_entries_outside_arena_rows_read_original(dtype):
+    """Negative entries of any value read the original K/V row, valid entries
+    their arena row. bf16 also: entries whose arena row would end beyond the
+    arena's first 4 GiB (2*(m+1)*row_bytes > 2^32) read the original row; the
+    fp32 kernel indexes the arena with any m >= 0, as the reference does, so
+    such entries are not given to it."""
+    frames, T, heads = 1, 700, 2
+    q, k, v = _inputs(frames, T, heads, seed=15, dtype=dtype)
+    base = _run(dtype, q, k, v, frames, T, heads, "cross")
+    rng = np.random.default_rng(16)
+    arena, kvmap = _random_arena(k.to(dtype), v.to(dtype), rng, frac=0.2)
+    odd = torch.from_numpy(rng.choice(T, size=200, replace=False))
+    vals = [-2, -7, -(1 << 40), -(1 << 63)]
+    if dtype == torch.bfloat16:
+        row_bytes = heads * 128 * 2
+        vals += [(1 << 31) // row_bytes, 1 << 31, (1 << 31) + 5, 1 << 40, 1 << 62]
+    specials = torch.tensor(vals, dtype=torch.int64)
+    kvmap[odd] = specials[torch.arange(200) % len(specials)]
+    got = _run(dtype, q, k, v, frames, T, heads, "cross", arena=arena.to(DEV).contiguous(),
+               kvmap=kvmap.to(DEV))
+    assert torch.equal(got, base)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 def test_c1_full_frame(dtype):
     """C1 shape: 1560 tokens x 12 heads x 128, policy none."""
     T, heads = 1560, 12
