@@ -99,44 +99,93 @@ void make_parent_dirs(const std::string& path) {
     }
 }
 
-}  // namespace
-
-int main(int argc, char** argv) {
-    std::string policy_name, q_path, k_path, v_path, csv_path, out_path;
-    std::string attn_mode = "intra", dtype_name = "fp32";
+// Command-line options. The flag names, meanings and defaults are the
+// reference driver's (src/run_policy_experiment.cu:77-95), so its scripts can
+// drive this binary; --dtype and --window are additions.
+struct Options {
+    std::string policy, attn_mode = "intra", q, k, v, motion_csv, out, dtype = "fp32";
     int streaming = 0, window = 0;
     long frames = 8, tokens = 1560, hidden = 1536, heads = 12;
     long tile_tokens = 16, set_aside = 2162688;
+};
+
+// One table entry per flag, with exactly one target; `--streaming` is a
+// switch, every other flag takes the next argument.
+struct FlagSpec {
+    const char* name;
+    std::string* text;
+    long* number;
+    int* flag;
+    bool is_switch;
+};
+
+bool parse_options(int argc, char** argv, Options& o) {
+    const FlagSpec table[] = {
+        {"--policy", &o.policy, nullptr, nullptr, false},
+        {"--attn-mode", &o.attn_mode, nullptr, nullptr, false},
+        {"--streaming", nullptr, nullptr, &o.streaming, true},
+        {"--q", &o.q, nullptr, nullptr, false},
+        {"--k", &o.k, nullptr, nullptr, false},
+        {"--v", &o.v, nullptr, nullptr, false},
+        {"--motion-csv", &o.motion_csv, nullptr, nullptr, false},
+        {"--out", &o.out, nullptr, nullptr, false},
+        {"--frames", nullptr, &o.frames, nullptr, false},
+        {"--tokens", nullptr, &o.tokens, nullptr, false},
+        {"--hidden", nullptr, &o.hidden, nullptr, false},
+        {"--heads", nullptr, &o.heads, nullptr, false},
+        {"--tile-tokens", nullptr, &o.tile_tokens, nullptr, false},
+        {"--set-aside-bytes", nullptr, &o.set_aside, nullptr, false},
+        {"--dtype", &o.dtype, nullptr, nullptr, false},
+        {"--window", nullptr, nullptr, &o.window, false},
+    };
     for (int i = 1; i < argc; ++i) {
-        std::string a = argv[i];
-        auto next = [&]() -> std::string {
-            if (i + 1 >= argc) {
-                fprintf(stderr, "missing value for %s\n", a.c_str());
-                exit(1);
-            }
-            return std::string(argv[++i]);
-        };
-        if (a == "--policy") policy_name = next();
-        else if (a == "--attn-mode") attn_mode = next();
-        else if (a == "--streaming") streaming = 1;
-        else if (a == "--q") q_path = next();
-        else if (a == "--k") k_path = next();
-        else if (a == "--v") v_path = next();
-        else if (a == "--motion-csv") csv_path = next();
-        else if (a == "--out") out_path = next();
-        else if (a == "--frames") frames = atol(next().c_str());
-        else if (a == "--tokens") tokens = atol(next().c_str());
-        else if (a == "--hidden") hidden = atol(next().c_str());
-        else if (a == "--heads") heads = atol(next().c_str());
-        else if (a == "--tile-tokens") tile_tokens = atol(next().c_str());
-        else if (a == "--set-aside-bytes") set_aside = atol(next().c_str());
-        else if (a == "--dtype") dtype_name = next();
-        else if (a == "--window") window = atoi(next().c_str());
-        else {
-            fprintf(stderr, "unknown arg %s\n", a.c_str());
-            return 1;
+        const FlagSpec* spec = nullptr;
+        for (const FlagSpec& f : table)
+            if (strcmp(argv[i], f.name) == 0) spec = &f;
+        if (!spec) {
+            fprintf(stderr, "unknown arg %s\n", argv[i]);
+            return false;
         }
+        if (spec->is_switch) {
+            *spec->flag = 1;
+            continue;
+        }
+        if (i + 1 >= argc) {
+            fprintf(stderr, "missing value for %s\n", spec->name);
+            return false;
+        }
+        const char* value = argv[++i];
+        if (spec->text) {
+            *spec->text = value;
+            continue;
+        }
+        char* end = nullptr;
+        errno = 0;
+        const long n = strtol(value, &end, 10);
+        if (errno != 0 || end == value || *end != '\0') {
+            fprintf(stderr, "%s needs an integer, got '%s'\n", spec->name, value);
+            return false;
+        }
+        if (spec->number)
+            *spec->number = n;
+        else
+            *spec->flag = (int)n;
     }
+    return true;
+}
+
+}  // namespace
+
+int main(int argc, char** argv) {
+    Options opt;
+    if (!parse_options(argc, argv, opt)) return 1;
+    const std::string& policy_name = opt.policy;
+    const std::string &q_path = opt.q, &k_path = opt.k, &v_path = opt.v;
+    const std::string &csv_path = opt.motion_csv, &out_path = opt.out;
+    const std::string &attn_mode = opt.attn_mode, &dtype_name = opt.dtype;
+    const int streaming = opt.streaming, window = opt.window;
+    const long frames = opt.frames, tokens = opt.tokens, hidden = opt.hidden, heads = opt.heads;
+    const long tile_tokens = opt.tile_tokens, set_aside = opt.set_aside;
     const bool xframe = attn_mode == "cross";
     const int dtype = dtype_name == "bf16" ? 1 : 0;
     if (dtype_name != "bf16" && dtype_name != "fp32") {
