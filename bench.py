@@ -15,6 +15,10 @@ dominant kernel (attn_fwd_bf16) from HIP events over its launches; and the
 CPU baseline: the oracle's PyTorch fp32 attention on a bounded sample of the
 same workload on this host's cores.
 
+Also reported under "kv_producer": the upstream K/V producer (the reference's
+DiT backbone forward, src/backbone.py:8-67) at the C3 frame set, whole
+forward and per stage, each stage against its roofline.
+
 python bench.py [--steps K] [--warmup W] [--policy P] [--layers L]
 """
 
@@ -53,6 +57,10 @@ def parse():
     ap.add_argument("--profile-policy", default=None,
                     help="run exactly one 30-layer step of this policy's pipeline and exit "
                          "(for rocprofv3 --pmc byte counting per policy)")
+    ap.add_argument("--no-producer", action="store_true",
+                    help="skip the upstream K/V producer measurement")
+    ap.add_argument("--producer-only", action="store_true",
+                    help="measure only the upstream K/V producer (prints its object) and exit")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="run 4 device-to-device copies of 256 MiB and exit (known-size "
                          "reference for FETCH_SIZE / WRITE_SIZE scaling)")
@@ -94,6 +102,151 @@ def cpu_baseline(cfg, units_target: int):
                       f"/ {cfg.frames} frames"}
 
 
+def producer_bench(args, torch, stream):
+    """Upstream K/V producer (reference: src/backbone.py:8-67) at the C3 frame
+    set: 8 frames x 1560 tokens, 30 layers, hidden 1536 = 12 x 128, latent
+    channels 16, bf16 projections with an fp32 residual stream.
+
+    Times the whole forward (W warmup, K timed, HIP events on the launch
+    stream), then each stage of a block over the 30 layers with events around
+    every launch: LayerNorm (fp32 -> bf16, HBM-bound), the three q/k/v
+    projections (hipBLASLt, MFMA-bound), intra-frame attention (all 8 frames
+    in one launch) and out_proj with the residual add."""
+    from kvpersist import api
+    from kvpersist import backbone as kb
+
+    frames, layers = 8, args.layers
+    cfg = kb.BackboneConfig(num_layers=layers)
+    T, D, H = cfg.tokens_per_frame, cfg.hidden_dim, cfg.num_heads
+    rows = frames * T
+    model = kb.SelfAttentionBackbone(cfg, seed=0, dtype="bf16")
+    gen = torch.Generator(device="cuda").manual_seed(7)
+    lat = torch.randn(frames, cfg.latent_channels, cfg.latent_grid_rows, cfg.latent_grid_cols,
+                      device="cuda", generator=gen)
+    torch.cuda.synchronize()
+
+    def ev():
+        return torch.cuda.Event(enable_timing=True)
+
+    for _ in range(max(1, args.warmup)):
+        out = model.forward_token_major(lat, stream=stream)
+    torch.cuda.synchronize()
+    e0, e1 = ev(), ev()
+    e0.record()
+    for _ in range(args.steps):
+        out = model.forward_token_major(lat, stream=stream)
+    e1.record()
+    torch.cuda.synchronize()
+    fwd_ms = e0.elapsed_time(e1) / args.steps
+    hidden, kk, vv, _ = out
+    finite = bool(torch.isfinite(hidden).all()) and bool(torch.isfinite(kk[-1].float()).all())
+    del out, hidden, kk, vv
+
+    # stage pass: the block's pieces on the model's own parameters
+    x = torch.randn(rows, D, device="cuda", generator=gen)
+    xn = torch.empty(rows, D, dtype=torch.bfloat16, device="cuda")
+    q, k, v, ctx = (torch.empty_like(xn) for _ in range(4))
+    P = {n: model.param_info(n)[0] for n in model.param_names()}
+    api.set_stream(stream)
+    stages = {"layer_norm": [], "qkv_proj": [], "attention": [], "out_proj": []}
+    for rep in range(2):  # the first pass warms plans and caches, the second is measured
+        for s in stages.values():
+            s.clear()
+        for layer in range(layers):
+            b = f"blocks.{layer}."
+            marks = [ev() for _ in range(5)]
+            marks[0].record()
+            kb.layer_norm(x, P[b + "norm.weight"], P[b + "norm.bias"], xn, stream=stream)
+            marks[1].record()
+            w = P[b + "attn.qkv_proj.weight"]
+            bias = P[b + "attn.qkv_proj.bias"]
+            for i, dst in enumerate((q, k, v)):  # row blocks of qkv_proj (bf16 W, fp32 b)
+                kb.linear(xn, w + i * D * D * 2, bias + i * D * 4, dst, stream=stream)
+            marks[2].record()
+            api.attn_forward_launcher_bf16(q, k, v, None, None, ctx, frames, T, D, H,
+                                           remap=False)
+            marks[3].record()
+            kb.linear(ctx, P[b + "attn.out_proj.weight"], P[b + "attn.out_proj.bias"], x,
+                      accumulate=True, stream=stream)
+            marks[4].record()
+            for j, name in enumerate(stages):
+                stages[name].append((marks[j], marks[j + 1]))
+        torch.cuda.synchronize()
+    api.set_stream(None)
+
+    def avg_ms(name):
+        pairs = stages[name]
+        return sum(a.elapsed_time(b) for a, b in pairs) / len(pairs)
+
+    ln_ms, qkv_ms = avg_ms("layer_norm"), avg_ms("qkv_proj")
+    att_ms, out_ms = avg_ms("attention"), avg_ms("out_proj")
+    ln_bytes = rows * D * (4 + 2) + 2 * D * 4
+    qkv_flops = 3 * 2 * rows * D * D
+    att_flops = frames * 4 * T * T * D
+    out_flops = 2 * rows * D * D
+
+    def roof(bound, amount, ms, unit_peak, unit, what):
+        ach = amount / (ms * 1e-3) / (1e9 if unit == "GB/s" else 1e12)
+        return {"bound": bound, "achieved": round(ach, 2), "peak": unit_peak, "unit": unit,
+                "frac": round(ach / unit_peak, 4), "avg_launch_ms": round(ms, 5),
+                "per_launch": what}
+
+    prod = {
+        "metric": "K/V producer ms/frame (30-layer forward, per-layer K/V into HBM)",
+        "value": round(fwd_ms / frames, 4),
+        "unit": "ms/frame",
+        "ms_per_forward": round(fwd_ms, 3),
+        "tokens_per_s": round(rows / (fwd_ms * 1e-3)),
+        "outputs_finite": finite,
+        "config": {"workload": "SelfAttentionBackbone forward, 8 frames x 1560 tokens, 30 layers, "
+                               "hidden 1536 (12 x 128), latent channels 16, bf16 projections, "
+                               "fp32 residual stream, random-init weights (seed 0)",
+                   "frames": frames, "layers": layers, "dtype": "bf16"},
+        "stages_ms_per_layer": {"layer_norm": round(ln_ms, 5), "qkv_proj": round(qkv_ms, 5),
+                                "attention": round(att_ms, 5), "out_proj": round(out_ms, 5)},
+        "rooflines": {
+            "layer_norm": roof("hbm", ln_bytes, ln_ms, HBM_PEAK_GBS, "GB/s",
+                               f"{ln_bytes} B (fp32 row in, bf16 row out, {rows} rows)"),
+            "qkv_proj": roof("mfma", qkv_flops, qkv_ms, BF16_PEAK_TFLOPS, "TFLOP/s",
+                             f"3 hipBLASLt GEMMs, {qkv_flops} flop"),
+            "attention": roof("mfma", att_flops, att_ms, BF16_PEAK_TFLOPS, "TFLOP/s",
+                              f"attn_fwd_bf16_kernel intra-frame, {frames} frames, "
+                              f"{att_flops} flop"),
+            "out_proj": roof("mfma", out_flops, out_ms, BF16_PEAK_TFLOPS, "TFLOP/s",
+                             f"1 hipBLASLt GEMM + residual, {out_flops} flop"),
+        },
+    }
+    if not args.no_cpu_baseline:
+        prod["cpu_baseline"] = producer_cpu_baseline(model, cfg, frames, layers)
+    model.close()
+    return prod
+
+
+def producer_cpu_baseline(model, cfg, frames, layers):
+    """Oracle block (float64 LN and projections, fp32 torch attention) for one
+    frame of one layer on host cores, scaled to ms per frame of the forward."""
+    import numpy as np
+    import torch
+    sys.path.insert(0, str(ROOT))
+    from oracle import backbone as ob
+    nthreads = min(16, os.cpu_count() or 1)
+    torch.set_num_threads(nthreads)
+    p = {n: model.get_param(n).numpy() for n in model.param_names()
+         if n.startswith("blocks.0.")}
+    T, D = cfg.tokens_per_frame, cfg.hidden_dim
+    x = np.random.default_rng(0).standard_normal((T, D)).astype(np.float32)
+    times = []
+    for _ in range(3):
+        t0 = time.perf_counter()
+        ob.block_forward(x, p, 0, 1, T, cfg.num_heads, bf16=True)
+        times.append(time.perf_counter() - t0)
+    per_fl = sorted(times)[1]
+    return {"value": round(per_fl * layers * 1e3, 3), "unit": "ms/frame", "cores": nthreads,
+            "kind": "port",
+            "sample": f"oracle block (LN + q/k/v projections + attention + out_proj), 1 frame x "
+                      f"1 layer, median of 3, x {layers} layers"}
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -116,6 +269,10 @@ def main():
             assert lib.kvp_memcpy_d2d(dst.data_ptr(), src.data_ptr(), nbytes, None) == 0
         torch.cuda.synchronize()
         print(json.dumps({"copy_calibration_bytes_per_copy": nbytes, "copies": 4}), flush=True)
+        return
+    if args.producer_only:
+        prod = producer_bench(args, torch, torch.cuda.current_stream().cuda_stream)
+        print(json.dumps({"kv_producer": prod}), flush=True)
         return
     cfg = workloads.CONFIGS["c3"]
     layers = args.layers
@@ -255,6 +412,12 @@ def main():
         cpu = cpu_baseline(cfg, args.cpu_sample_units)
         log(f"cpu baseline {cpu['value']} ms/frame on {cpu['cores']} cores")
 
+    prod = None
+    if not args.no_producer:
+        log("upstream K/V producer ...")
+        prod = producer_bench(args, torch, stream)
+        log(f"producer {prod['value']} ms/frame")
+
     value = ms_step / F
     line = {
         "metric": METRIC,
@@ -292,6 +455,7 @@ def main():
         "cpu_baseline": cpu,
         "policies": policies,
         "wall_ms_per_step": round(wall_step, 3),
+        "kv_producer": prod,
     }
     print(json.dumps(line), flush=True)
     main_pl.close()

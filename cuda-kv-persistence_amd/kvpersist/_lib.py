@@ -24,7 +24,7 @@ c_long_p = ctypes.POINTER(ctypes.c_long)
 c_int_p = ctypes.POINTER(ctypes.c_int)
 c_size_t = ctypes.c_size_t
 
-# name -> (restype, argtypes); every symbol declared in include/kvp_c_api.h.
+# name -> (restype, argtypes); every symbol declared in include/*.h.
 SIGNATURES = {
     # KVTileManager facade (reference: src/kv_tile_manager.cu:223-341)
     "kvtm_create": (c_void_p, [c_long, c_long]),
@@ -120,6 +120,26 @@ SIGNATURES = {
     "kvp_pipeline_arena": (c_void_p, [c_void_p]),
     "kvp_pipeline_device_map": (c_void_p, [c_void_p]),
     "kvp_pipeline_manager": (c_void_p, [c_void_p]),
+    # upstream K/V producer (reference: src/backbone.py:8-67), include/kvp_producer.h
+    "kvp_layer_norm": (c_int, [c_int, c_int, c_void_p, c_void_p, c_void_p, c_void_p, c_long,
+                               c_int, ctypes.c_float, c_void_p]),
+    "kvp_linear": (c_int, [c_int, c_int, c_void_p, c_void_p, c_void_p, c_void_p, c_long, c_int,
+                           c_int, c_int, c_void_p]),
+    "kvp_qkv_project": (c_int, [c_int, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
+                                c_void_p, c_void_p, c_void_p, c_void_p, c_long, c_int,
+                                c_void_p]),
+    "kvp_backbone_create": (c_void_p, [c_int, c_int, c_int, c_int, c_int, c_int,
+                                       ctypes.c_ulong]),
+    "kvp_backbone_destroy": (None, [c_void_p]),
+    "kvp_backbone_param_count": (c_long, [c_void_p]),
+    "kvp_backbone_num_tensors": (c_int, [c_void_p]),
+    "kvp_backbone_tensor_name": (c_char_p, [c_void_p, c_int]),
+    "kvp_backbone_param_info": (c_int, [c_void_p, c_char_p, ctypes.POINTER(c_void_p), c_long_p,
+                                        c_int_p]),
+    "kvp_backbone_set_param": (c_int, [c_void_p, c_char_p, c_float_p, c_long]),
+    "kvp_backbone_get_param": (c_int, [c_void_p, c_char_p, c_float_p, c_long]),
+    "kvp_backbone_forward": (c_int, [c_void_p, c_void_p, c_int, c_void_p, c_void_p, c_void_p,
+                                     c_void_p, c_long, c_void_p]),
 }
 
 _LIB = None

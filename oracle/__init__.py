@@ -18,6 +18,9 @@ Modules
               regenerate the 8-frame seed-42 trace whose golden statistics
               the reference publishes (reference:
               traces/gen_synthetic_motion.py:41-89).
+  backbone    the upstream K/V producer: LayerNorm, the q/k/v projections,
+              the DiT block and the backbone forward in float64
+              (reference: src/backbone.py:8-67).
   ref_build   recipe compiling the reference's own policy source into
               oracle/_ref/ (this container only; never shipped).
 

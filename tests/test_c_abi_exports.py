@@ -18,7 +18,7 @@ INCLUDE = ROOT / "include"
 
 
 def _c_api_names():
-    text = (INCLUDE / "kvp_c_api.h").read_text()
+    text = "\n".join(p.read_text() for p in sorted(INCLUDE.glob("kvp_*.h")))
     text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
     names = set()
     for m in re.finditer(r"^\s*[A-Za-z_][\w\s\*]*?\b(kv[a-z_0-9]+)\s*\(", text, flags=re.M):

@@ -1,0 +1,331 @@
+"""GPU parity of the upstream K/V producer (include/kvp_producer.h) against
+oracle/backbone.py, through the C-ABI.
+
+Tolerances: fp32 max-abs <= 1e-3 and mean-abs <= 1e-4 on K/V and hidden
+(the north-star fp32 bar); bf16 max-abs <= 2e-2 against the oracle run with
+the same bf16 storage points. Single ops are held tighter: fp32 LayerNorm
+within 2e-5, fp32 linear within 1e-4, bf16 outputs within one bf16 ulp.
+
+The reference's own backbone tests are restated for this implementation
+(reference: tests/test_skeleton.py:19-72): config invariants, the parameter
+count, per-layer K/V shapes (b, heads, t, head_dim), seeded reproducibility.
+"""
+
+import numpy as np
+import pytest
+import torch
+from scipy import stats
+
+from kvpersist import FramePipeline, _lib
+from kvpersist import backbone as kb
+from oracle import attention as at
+from oracle import backbone as ob
+
+DEV = "cuda"
+FP32_MAX, FP32_MEAN, BF16_MAX = 1e-3, 1e-4, 2e-2
+TDT = {0: torch.float32, 1: torch.bfloat16}
+
+
+def _err(got, want):
+    e = np.abs(np.asarray(got, np.float64) - np.asarray(want, np.float64))
+    return float(e.max()), float(e.mean())
+
+
+def _bf16_close(got, want, what=""):
+    """Within one bf16 ulp of the wide value (rounding of a nearby wide value)."""
+    got = np.asarray(got, np.float64)
+    want = np.asarray(want, np.float64)
+    bad = np.abs(got - want) > np.abs(want) * 2.0 ** -7 + 1e-5
+    assert not bad.any(), (what, int(bad.sum()), got[bad][:4], want[bad][:4])
+
+
+# ------------------------------------------------------------------ layer norm
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("in_dt,out_dt", [(0, 0), (0, 1), (1, 0), (1, 1)])
+@pytest.mark.parametrize("rows,D", [(3, 4), (5, 132), (1560, 1536), (65, 4096), (1, 2048)])
+def test_layer_norm_matches_oracle(in_dt, out_dt, rows, D):
+    print(f"layer_norm in={in_dt} out={out_dt} rows={rows} D={D}", flush=True)
+    rng = np.random.default_rng(rows * 7 + D)
+    x = (rng.standard_normal((rows, D)) * 2 + rng.standard_normal((rows, 1))).astype(np.float32)
+    if in_dt == 1:
+        x = ob.round_bf16(x)
+    g = (1 + 0.1 * rng.standard_normal(D)).astype(np.float32)
+    b = (0.1 * rng.standard_normal(D)).astype(np.float32)
+    xd = torch.from_numpy(x).to(DEV).to(TDT[in_dt])
+    y = torch.empty(rows, D, dtype=TDT[out_dt], device=DEV)
+    kb.layer_norm(xd, torch.from_numpy(g).to(DEV), torch.from_numpy(b).to(DEV), y)
+    torch.cuda.synchronize()
+    want = ob.layer_norm(x, g, b)
+    got = y.float().cpu().numpy()
+    if out_dt == 0:
+        assert _err(got, want)[0] <= 2e-5
+    else:
+        _bf16_close(got, want, "layer_norm bf16")
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("c", [7.25, -3.5, 0.0])
+def test_layer_norm_constant_row_gives_beta_exactly(c):
+    """Rows of one exactly-summable value have an exact fp32 mean, so the
+    output is beta bit for bit (fp32 out)."""
+    D = 1536
+    rng = np.random.default_rng(1)
+    g = rng.standard_normal(D).astype(np.float32)
+    b = rng.standard_normal(D).astype(np.float32)
+    x = torch.full((4, D), c, dtype=torch.float32, device=DEV)
+    y = torch.empty_like(x)
+    kb.layer_norm(x, torch.from_numpy(g).to(DEV), torch.from_numpy(b).to(DEV), y)
+    torch.cuda.synchronize()
+    assert torch.equal(y.cpu(), torch.from_numpy(b).expand(4, D))
+
+
+def test_producer_rejects_bad_arguments(lib):
+    """Argument errors are reported before any device work (runs without a GPU)."""
+    assert lib.kvp_layer_norm(0, 0, 16, 16, 16, 16, 4, 6, 1e-5, None) != 0
+    assert "multiple of 4" in _lib.last_error()
+    assert lib.kvp_layer_norm(2, 0, 16, 16, 16, 16, 4, 8, 1e-5, None) != 0
+    assert lib.kvp_linear(0, 1, 16, 16, None, 16, 4, 8, 8, 0, None) != 0
+    assert "not supported" in _lib.last_error()
+    assert lib.kvp_linear(0, 0, 16, 16, None, 16, 0, 8, 8, 0, None) != 0
+    assert lib.kvp_qkv_project(3, 16, 16, 16, 16, 16, 16, 16, 16, 16, 4, 128, None) != 0
+    assert not lib.kvp_backbone_create(0, 2, 16, 1000, 12, 16, 0)
+    assert "heads * 128" in _lib.last_error()
+    assert not lib.kvp_backbone_create(2, 2, 16, 256, 2, 16, 0)
+    assert lib.kvp_backbone_forward(None, None, 1, None, None, None, None, 0, None) != 0
+
+
+def test_config_and_constructor_mirror_reference():
+    """Reference: tests/test_skeleton.py:19-25,69-72 (no GPU needed)."""
+    cfg = kb.BackboneConfig()
+    assert cfg.num_heads * cfg.head_dim == cfg.hidden_dim == 1536
+    assert cfg.latent_grid_rows * cfg.latent_grid_cols == cfg.tokens_per_frame == 1560
+    assert cfg.num_layers == 30
+    with pytest.raises(ValueError):
+        kb.BackboneConfig(hidden_dim=1000, num_heads=12, head_dim=128)
+    with pytest.raises(ValueError):
+        kb.BackboneConfig(latent_grid_rows=31)
+    with pytest.raises(NotImplementedError):
+        kb.SelfAttentionBackbone(init="pretrained")
+    with pytest.raises(ValueError):
+        kb.SelfAttentionBackbone(kb.BackboneConfig(hidden_dim=768, num_heads=12, head_dim=64))
+
+
+# ------------------------------------------------------------------ linear
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("in_dt,out_dt,acc", [(0, 0, False), (0, 0, True), (1, 1, False),
+                                              (1, 0, True), (1, 0, False)])
+@pytest.mark.parametrize("rows,K,N,bias", [(1, 16, 1536, True), (77, 256, 384, True),
+                                           (1560, 1536, 1536, True), (300, 1536, 1536, False)])
+def test_linear_matches_oracle(in_dt, out_dt, acc, rows, K, N, bias):
+    print(f"linear in={in_dt} out={out_dt} acc={acc} rows={rows} K={K} N={N}", flush=True)
+    rng = np.random.default_rng(rows + K + N)
+    x = rng.standard_normal((rows, K)).astype(np.float32)
+    w = (0.02 * rng.standard_normal((N, K))).astype(np.float32)
+    if in_dt == 1:
+        x, w = ob.round_bf16(x), ob.round_bf16(w)
+    b = (0.1 * rng.standard_normal(N)).astype(np.float32) if bias else None
+    y0 = rng.standard_normal((rows, N)).astype(np.float32)
+    if out_dt == 1:
+        y0 = ob.round_bf16(y0)
+    y = torch.from_numpy(y0).to(DEV).to(TDT[out_dt])
+    kb.linear(torch.from_numpy(x).to(DEV).to(TDT[in_dt]), torch.from_numpy(w).to(DEV).to(TDT[in_dt]),
+              None if b is None else torch.from_numpy(b).to(DEV), y, accumulate=acc)
+    torch.cuda.synchronize()
+    want = ob.linear(x, w, b) + (y0 if acc else 0)
+    got = y.float().cpu().numpy()
+    if out_dt == 0:
+        assert _err(got, want)[0] <= 1e-4
+    else:
+        _bf16_close(got, want, "linear bf16")
+
+
+# ------------------------------------------------------------------ qkv projection
+
+def _params_from(model):
+    return {n: t.numpy().astype(np.float32) for n, t in model.state_dict().items()}
+
+
+def _cfg(layers, T, heads):
+    rows, cols = {200: (10, 20), 1560: (30, 52), 64: (8, 8)}[T]
+    return kb.BackboneConfig(num_layers=layers, hidden_dim=heads * 128, num_heads=heads,
+                             tokens_per_frame=T, latent_grid_rows=rows, latent_grid_cols=cols)
+
+
+def _ocfg(cfg):
+    return ob.Config(num_layers=cfg.num_layers, hidden_dim=cfg.hidden_dim,
+                     num_heads=cfg.num_heads, tokens_per_frame=cfg.tokens_per_frame,
+                     latent_channels=cfg.latent_channels)
+
+
+def _randomise(model, rng):
+    """Non-trivial LayerNorm affines and biases, so every parameter matters."""
+    for n in model.param_names():
+        if n.endswith("norm.weight"):
+            model.set_param(n, 1 + 0.1 * rng.standard_normal(model.param_info(n)[1]))
+        elif n.endswith("bias"):
+            model.set_param(n, 0.05 * rng.standard_normal(model.param_info(n)[1]))
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("dtype", [0, 1])
+@pytest.mark.parametrize("rows,heads", [(300, 2), (1560, 12)])
+def test_qkv_project_matches_oracle(dtype, rows, heads):
+    print(f"qkv_project dtype={dtype} rows={rows} heads={heads}", flush=True)
+    D = heads * 128
+    model = kb.SelfAttentionBackbone(_cfg(1, 64, heads), seed=3, dtype=dtype)
+    rng = np.random.default_rng(rows)
+    _randomise(model, rng)
+    p = _params_from(model)
+    x = rng.standard_normal((rows, D)).astype(np.float32)
+    xd = torch.from_numpy(x).to(DEV)
+    dt = TDT[dtype]
+    xn = torch.empty(rows, D, dtype=dt, device=DEV)
+    q, k, v = (torch.empty(rows, D, dtype=dt, device=DEV) for _ in range(3))
+    ptr = {n: model.param_info(n)[0] for n in model.param_names()}
+    kb.qkv_project(xd, ptr["blocks.0.norm.weight"], ptr["blocks.0.norm.bias"],
+                   ptr["blocks.0.attn.qkv_proj.weight"], ptr["blocks.0.attn.qkv_proj.bias"],
+                   xn, q, k, v)
+    torch.cuda.synchronize()
+    want = ob.qkv_project(x, p, 0, D, bf16=dtype == 1)
+    for name, got, w in zip("qkv", (q, k, v), want):
+        mx, mean = _err(got.float().cpu().numpy(), w)
+        if dtype == 0:
+            assert mx <= 1e-4, (name, mx)
+        else:
+            assert mx <= BF16_MAX and mean <= 1e-3, (name, mx, mean)
+
+
+# ------------------------------------------------------------------ backbone
+
+def _check(got, want, dtype, what):
+    mx, mean = _err(got, want)
+    if dtype == 0:
+        assert mx <= FP32_MAX and mean <= FP32_MEAN, (what, mx, mean)
+    else:
+        assert mx <= BF16_MAX, (what, mx, mean)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("dtype", [0, 1])
+@pytest.mark.parametrize("frames,T,heads,layers", [(2, 200, 2, 2), (1, 1560, 12, 2)])
+def test_backbone_matches_oracle(dtype, frames, T, heads, layers):
+    print(f"backbone dtype={dtype} frames={frames} T={T} heads={heads} layers={layers}",
+          flush=True)
+    torch.set_num_threads(min(16, max(1, torch.get_num_threads())))
+    cfg = _cfg(layers, T, heads)
+    model = kb.SelfAttentionBackbone(cfg, seed=11, dtype=dtype)
+    rng = np.random.default_rng(T + heads)
+    _randomise(model, rng)
+    p = _params_from(model)
+    lat = rng.standard_normal((frames, 16, cfg.latent_grid_rows, cfg.latent_grid_cols))
+    lat = lat.astype(np.float32)
+    hidden, k, v, q = model.forward_token_major(torch.from_numpy(lat).to(DEV), keep_q=True)
+    torch.cuda.synchronize()
+    want_h, per_layer = ob.backbone_forward(lat, p, _ocfg(cfg), frames, bf16=dtype == 1)
+    for l, (qw, kw, vw) in enumerate(per_layer):
+        _check(q[l].float().cpu().numpy(), qw, dtype, f"q{l}")
+        _check(k[l].float().cpu().numpy(), kw, dtype, f"k{l}")
+        _check(v[l].float().cpu().numpy(), vw, dtype, f"v{l}")
+    _check(hidden.cpu().numpy(), want_h, dtype, "hidden")
+
+
+@pytest.mark.gpu
+def test_reference_config_forward_shapes_and_reproducibility():
+    """Default config, seed 0 (reference: tests/test_skeleton.py:46-67): hidden
+    (1, 1560, 1536), 30 (k, v) pairs of (1, 12, 1560, 128) fp32; equal seeds
+    give equal parameters and bitwise-equal outputs, another seed does not;
+    layer 0's K/V match the oracle."""
+    cfg = kb.BackboneConfig()
+    a = kb.SelfAttentionBackbone(cfg, seed=123)
+    b = kb.SelfAttentionBackbone(cfg, seed=123)
+    c = kb.SelfAttentionBackbone(cfg, seed=124)
+    assert a.param_count() == 283_421_184
+    for n in ("token_embed.weight", "blocks.7.attn.qkv_proj.weight", "blocks.29.attn.out_proj.weight"):
+        assert torch.equal(a.get_param(n), b.get_param(n))
+        assert not torch.equal(a.get_param(n), c.get_param(n))
+    torch.manual_seed(0)
+    lat = torch.randn(1, cfg.latent_channels, cfg.latent_grid_rows, cfg.latent_grid_cols,
+                      device=DEV)
+    hidden, kv = a(lat, timestep=torch.zeros(1), context=None)
+    hidden2, kv2 = b(lat)
+    torch.cuda.synchronize()
+    assert hidden.shape == (1, cfg.tokens_per_frame, cfg.hidden_dim)
+    assert len(kv) == cfg.num_layers
+    for (k, v), (k2, v2) in zip(kv, kv2):
+        assert k.shape == v.shape == (1, cfg.num_heads, cfg.tokens_per_frame, cfg.head_dim)
+        assert k.dtype == torch.float32
+        assert torch.equal(k, k2) and torch.equal(v, v2)
+    assert torch.equal(hidden, hidden2)
+    assert torch.isfinite(hidden).all()
+    p = {n: a.get_param(n).numpy() for n in ("blocks.0.norm.weight", "blocks.0.norm.bias",
+                                              "blocks.0.attn.qkv_proj.weight",
+                                              "blocks.0.attn.qkv_proj.bias",
+                                              "token_embed.weight", "token_embed.bias")}
+    x0 = ob.linear(lat.cpu().numpy().reshape(1560, 16), p["token_embed.weight"],
+                   p["token_embed.bias"]).astype(np.float32)
+    _, kw, vw = ob.qkv_project(x0, p, 0, cfg.hidden_dim)
+    k0 = kv[0][0].permute(0, 2, 1, 3).reshape(1560, 1536).cpu().numpy()
+    v0 = kv[0][1].permute(0, 2, 1, 3).reshape(1560, 1536).cpu().numpy()
+    _check(k0, kw, 0, "k0")
+    _check(v0, vw, 0, "v0")
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("dtype", [0, 1])
+def test_init_distributions(dtype):
+    """Linear weights normal(0, 0.02), Linear biases 0, LayerNorm weight 1 and
+    bias 0 (reference: src/backbone.py:51-56 and nn.LayerNorm's init)."""
+    model = kb.SelfAttentionBackbone(_cfg(2, 64, 12), seed=5, dtype=dtype)
+    w = model.get_param("blocks.1.attn.qkv_proj.weight").numpy().ravel()
+    n = w.size
+    assert abs(w.mean()) < 5 * 0.02 / np.sqrt(n)
+    assert abs(w.std() / 0.02 - 1) < 0.01
+    if dtype == 0:
+        assert stats.kstest(w[:200_000] / 0.02, "norm").pvalue > 1e-3
+    e = model.get_param("token_embed.weight").numpy()
+    assert abs(e.std() / 0.02 - 1) < 0.05
+    for name in ("token_embed.bias", "blocks.0.attn.qkv_proj.bias", "blocks.1.attn.out_proj.bias",
+                 "blocks.0.norm.bias", "final_norm.bias"):
+        assert not model.get_param(name).any(), name
+    for name in ("blocks.0.norm.weight", "blocks.1.norm.weight", "final_norm.weight"):
+        assert (model.get_param(name) == 1).all(), name
+    # different parameters draw different streams
+    a = model.get_param("blocks.0.attn.out_proj.weight")
+    b = model.get_param("blocks.1.attn.out_proj.weight")
+    assert not torch.equal(a, b)
+
+
+@pytest.mark.gpu
+def test_produced_kv_feed_the_arena_pipeline():
+    """Layer 1 K/V of a bf16 backbone run through the motion-gated cross-frame
+    pipeline: bitwise equal to policy none, and within the bf16 bar of the
+    oracle attention of the same q/k/v."""
+    torch.set_num_threads(min(16, max(1, torch.get_num_threads())))
+    frames, T, heads = 3, 1560, 12
+    D = heads * 128
+    cfg = _cfg(2, T, heads)
+    model = kb.SelfAttentionBackbone(cfg, seed=21, dtype="bf16")
+    rng = np.random.default_rng(22)
+    lat = torch.from_numpy(rng.standard_normal((frames, 16, 30, 52)).astype(np.float32)).to(DEV)
+    _, k, v, q = model.forward_token_major(lat, keep_q=True)
+    ql, kl, vl = q[1].contiguous(), k[1].contiguous(), v[1].contiguous()
+    tiles = (T + 15) // 16
+    scores = rng.random(frames * tiles, dtype=np.float32)
+    outs = {}
+    for policy, aside in (("none", 0), ("motion", 64 * 16 * 2 * D * 2)):
+        pl = FramePipeline(policy, cross=True, streaming=False, frames=frames, T=T, D=D,
+                           heads=heads, tile_tokens=16, set_aside_bytes=aside, dtype=1)
+        pl.set_scores(scores)
+        out = torch.empty_like(ql)
+        pl.run(ql, kl, vl, out)
+        torch.cuda.synchronize()
+        if policy == "motion":
+            assert pl.staged_tiles() > 0
+        outs[policy] = out.cpu()
+        pl.close()
+    assert torch.equal(outs["none"], outs["motion"])
+    want = at.attention_frames(ql.float().cpu(), kl.float().cpu(), vl.float().cpu(), frames, T,
+                               heads, "cross")
+    assert float((outs["none"].float() - want).abs().max()) <= BF16_MAX
