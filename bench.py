@@ -110,8 +110,9 @@ def producer_bench(args, torch, stream):
     Times the whole forward (W warmup, K timed, HIP events on the launch
     stream), then each stage of a block over the 30 layers with events around
     every launch: LayerNorm (fp32 -> bf16, HBM-bound), the three q/k/v
-    projections (hipBLASLt, MFMA-bound), intra-frame attention (all 8 frames
-    in one launch) and out_proj with the residual add."""
+    projections (one launch of the grouped proj_gemm kernel, MFMA-bound),
+    intra-frame attention (all 8 frames in one launch) and out_proj with the
+    residual add (hipBLASLt)."""
     from kvpersist import api
     from kvpersist import backbone as kb
 
@@ -158,10 +159,10 @@ def producer_bench(args, torch, stream):
             marks[0].record()
             kb.layer_norm(x, P[b + "norm.weight"], P[b + "norm.bias"], xn, stream=stream)
             marks[1].record()
-            w = P[b + "attn.qkv_proj.weight"]
-            bias = P[b + "attn.qkv_proj.bias"]
-            for i, dst in enumerate((q, k, v)):  # row blocks of qkv_proj (bf16 W, fp32 b)
-                kb.linear(xn, w + i * D * D * 2, bias + i * D * 4, dst, stream=stream)
+            # the three row blocks of qkv_proj in one grouped launch, as the
+            # backbone runs them
+            kb.proj_gemm(xn, P[b + "attn.qkv_proj.weight"], P[b + "attn.qkv_proj.bias"],
+                         [q, k, v], tile_n=256, stream=stream)
             marks[2].record()
             api.attn_forward_launcher_bf16(q, k, v, None, None, ctx, frames, T, D, H,
                                            remap=False)
@@ -208,7 +209,7 @@ def producer_bench(args, torch, stream):
             "layer_norm": roof("hbm", ln_bytes, ln_ms, HBM_PEAK_GBS, "GB/s",
                                f"{ln_bytes} B (fp32 row in, bf16 row out, {rows} rows)"),
             "qkv_proj": roof("mfma", qkv_flops, qkv_ms, BF16_PEAK_TFLOPS, "TFLOP/s",
-                             f"3 hipBLASLt GEMMs, {qkv_flops} flop"),
+                             f"proj_gemm_bf16_kernel, 3 groups in one launch, {qkv_flops} flop"),
             "attention": roof("mfma", att_flops, att_ms, BF16_PEAK_TFLOPS, "TFLOP/s",
                               f"attn_fwd_bf16_kernel intra-frame, {frames} frames, "
                               f"{att_flops} flop"),

@@ -454,6 +454,15 @@ int qkv_project_impl(int dtype, const float* x, const float* ln_w, const float* 
         return 1;
     }
     if (layer_norm_impl(0, dtype, x, ln_w, ln_b, xn, rows, D, kLnEps, stream)) return 1;
+    if (dtype == 1) {
+        // bf16: one launch of the grouped projection kernel writes q, k and v
+        void* outs[3] = {q, k, v};
+        const int tile = D % 256 == 0 ? 256 : 128;
+        const int rc = launch_proj_gemm(xn, w_qkv, b_qkv, outs, 3, rows, D, D, 1, false, tile,
+                                        stream);
+        if (rc != 2) return rc;  // 2: shape outside the kernel's tiling, use hipBLASLt
+        clear_error();
+    }
     const size_t es = dtype_size(dtype);
     void* outs[3] = {q, k, v};
     for (int i = 0; i < 3; ++i) {

@@ -125,6 +125,8 @@ SIGNATURES = {
                                c_int, ctypes.c_float, c_void_p]),
     "kvp_linear": (c_int, [c_int, c_int, c_void_p, c_void_p, c_void_p, c_void_p, c_long, c_int,
                            c_int, c_int, c_void_p]),
+    "kvp_proj_gemm": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
+                              c_int, c_long, c_int, c_int, c_int, c_int, c_int, c_void_p]),
     "kvp_qkv_project": (c_int, [c_int, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
                                 c_void_p, c_void_p, c_void_p, c_void_p, c_long, c_int,
                                 c_void_p]),

@@ -96,6 +96,20 @@ def linear(x: torch.Tensor, weight, bias, out: torch.Tensor, accumulate: bool = 
     return out
 
 
+def proj_gemm(x: torch.Tensor, weight, bias, outs, accumulate: bool = False, tile_n: int = 256,
+              stream: int | None = None) -> None:
+    """Grouped projection on the hand-written kernel: outs[g] (+)= x W_g^T + b_g
+    with W_g the g-th [N]-row block of weight (bf16) and N = outs[0].shape[-1]."""
+    outs = list(outs)
+    n = outs[0].shape[-1]
+    k = x.shape[-1]
+    ptrs = [_ptr(o) for o in outs] + [None] * (3 - len(outs))
+    _check(_lib.load().kvp_proj_gemm(_ptr(x), _ptr(weight), _ptr(bias), ptrs[0], ptrs[1],
+                                     ptrs[2], len(outs), x.numel() // k, k, n,
+                                     _code_of(outs[0]), int(accumulate), tile_n, stream),
+           "kvp_proj_gemm")
+
+
 def qkv_project(x: torch.Tensor, ln_weight, ln_bias, qkv_weight, qkv_bias, xn, q, k, v,
                 stream: int | None = None) -> None:
     """LN(x) then q, k, v = the three [D]-row blocks of qkv_proj (x fp32 [rows, D])."""

@@ -38,6 +38,21 @@ int kvp_linear(int in_dtype, int out_dtype, const void* x, const void* w,
                const float* bias, void* y, long rows, int in_features,
                int out_features, int accumulate, void* stream);
 
+/* Grouped bf16 projection on this library's gfx950 MFMA kernel: for
+ * g < groups (1..3), out_g[r, n] = x[r, :] . w[g*N + n, :] + bias[g*N + n]
+ * (+ out_g[r, n] when accumulate != 0). x [rows, K] and w [groups*N, K]
+ * bf16, bias fp32 [groups*N] or NULL, out_g [rows, N] bf16 (out_dtype 1) or
+ * fp32 (out_dtype 0, the only one that may accumulate). One launch serves
+ * all groups: the q/k/v row blocks of qkv_proj written to three outputs, or
+ * out_proj added into the fp32 residual stream (reference:
+ * src/backbone.py:13-14,18-22,32-33). K a multiple of 64, N a multiple of
+ * tile_n (128 or 256 features per workgroup tile). Unused outputs may be
+ * NULL. */
+int kvp_proj_gemm(const void* x, const void* w, const float* bias,
+                  void* out0, void* out1, void* out2, int groups, long rows,
+                  int K, int N, int out_dtype, int accumulate, int tile_n,
+                  void* stream);
+
 /* One block's LayerNorm + qkv_proj (reference: src/backbone.py:13,18-19,32):
  * xn = LN(x) (x fp32 residual stream [rows, D]), then q, k, v [rows, D] =
  * xn W_{q,k,v}^T + b_{q,k,v} with W = qkv_weight [3D, D] (rows 0..D-1 -> q,
