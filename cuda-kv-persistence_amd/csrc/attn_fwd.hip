@@ -72,7 +72,8 @@ struct AttnArgs {
     const void* arena;
     const long* kvmap;
     void* out;
-    float* part_o;    // [splits][frames][nq][D] normalised partial O
+    void* part_o;     // [splits][frames][nq][D] normalised partial O:
+                      // fp16 from the bf16 kernel, fp32 from the fp32 kernel
     float* part_lse;  // [splits][frames][heads][nq] log2-sum-exp
     long q_fstride;   // elements between frames of q / out
     long kv_fstride;  // elements between frames of k / v
@@ -123,61 +124,29 @@ __device__ __forceinline__ float fast_exp2(float x) {
     return __builtin_amdgcn_exp2f(x);
 }
 
-// Writes the normalised result (or the split partial) of one wave.
-// o[nb][v] holds O^T[d = 32*nb + 8*(v/4) + 4*hh + v%4][q].
-template <typename OutT>
-__device__ __forceinline__ void store_rows(const AttnArgs& a, const WgCoord& c,
-                                           int q, int hh, const f32x16 (&o)[4],
-                                           float m_run, float l_run) {
+// fp32 kernel epilogue: writes the normalised result (or the fp32 split
+// partial) of one wave. o[nb][v] holds O^T[d = 32*nb + 8*(v/4) + 4*hh + v%4][q].
+__device__ __forceinline__ void store_rows_f32(const AttnArgs& a, const WgCoord& c, int q, int hh,
+                                               const f32x16 (&o)[4], float m_run, float l_run) {
     if (q >= a.nq) return;
     const float inv_l = 1.0f / l_run;
     const int col0 = c.head * kHeadDim + 4 * hh;
-    if (a.splits == 1) {
-        OutT* out = reinterpret_cast<OutT*>(a.out) + (long)c.frame * a.q_fstride +
-                    (long)q * a.D + col0;
+    const bool split = a.splits > 1;
+    const long slab = (long)c.split * a.frames + c.frame;
+    float* dst = split ? static_cast<float*>(a.part_o) + (slab * a.nq + q) * (long)a.D + col0
+                       : reinterpret_cast<float*>(a.out) + (long)c.frame * a.q_fstride +
+                             (long)q * a.D + col0;
 #pragma unroll
-        for (int nb = 0; nb < 4; ++nb) {
+    for (int nb = 0; nb < 4; ++nb) {
 #pragma unroll
-            for (int g = 0; g < 4; ++g) {
-                const int d = 32 * nb + 8 * g;
-                if constexpr (sizeof(OutT) == 4) {
-                    f32x4 w;
-                    w[0] = o[nb][4 * g + 0] * inv_l;
-                    w[1] = o[nb][4 * g + 1] * inv_l;
-                    w[2] = o[nb][4 * g + 2] * inv_l;
-                    w[3] = o[nb][4 * g + 3] * inv_l;
-                    *reinterpret_cast<f32x4*>(out + d) = w;
-                } else {
-                    typedef __attribute__((ext_vector_type(4))) __bf16 bf16x4;
-                    bf16x4 w;
-                    w[0] = (__bf16)(o[nb][4 * g + 0] * inv_l);
-                    w[1] = (__bf16)(o[nb][4 * g + 1] * inv_l);
-                    w[2] = (__bf16)(o[nb][4 * g + 2] * inv_l);
-                    w[3] = (__bf16)(o[nb][4 * g + 3] * inv_l);
-                    *reinterpret_cast<bf16x4*>(out + d) = w;
-                }
-            }
-        }
-    } else {
-        const long slab = (long)c.split * a.frames + c.frame;
-        float* po = a.part_o + (slab * a.nq + q) * (long)a.D + col0;
-#pragma unroll
-        for (int nb = 0; nb < 4; ++nb) {
-#pragma unroll
-            for (int g = 0; g < 4; ++g) {
-                f32x4 w;
-                w[0] = o[nb][4 * g + 0] * inv_l;
-                w[1] = o[nb][4 * g + 1] * inv_l;
-                w[2] = o[nb][4 * g + 2] * inv_l;
-                w[3] = o[nb][4 * g + 3] * inv_l;
-                *reinterpret_cast<f32x4*>(po + 32 * nb + 8 * g) = w;
-            }
-        }
-        if (hh == 0) {
-            a.part_lse[(slab * a.heads + c.head) * (long)a.nq + q] =
-                m_run + __log2f(l_run);
+        for (int g = 0; g < 4; ++g) {
+            const f32x4 w = {o[nb][4 * g + 0] * inv_l, o[nb][4 * g + 1] * inv_l,
+                             o[nb][4 * g + 2] * inv_l, o[nb][4 * g + 3] * inv_l};
+            *reinterpret_cast<f32x4*>(dst + 32 * nb + 8 * g) = w;
         }
     }
+    if (split && hh == 0)
+        a.part_lse[(slab * a.heads + c.head) * (long)a.nq + q] = m_run + __log2f(l_run);
 }
 
 // One online-softmax update for a lane's query over n fp32 scores held in
@@ -317,6 +286,50 @@ __device__ __forceinline__ void lgkm_wait_tr_n(u32x2& a, u32x2& b, u32x2& c, u32
 
 __device__ __forceinline__ void lgkm_wait_tr(u32x2& a, u32x2& b, u32x2& c, u32x2& d) {
     asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(a), "+v"(b), "+v"(c), "+v"(d)::"memory");
+}
+
+// bf16 kernel epilogue: the wave's 32 query rows x 128 dims go out as
+// 2-byte elements (fp16 split partials, or the bf16 output when the key range
+// is not split). They are staged in LDS as query rows of 256 B (16-byte
+// chunks XOR-swizzled by row & 15) and stored as full rows, 16 bytes per
+// lane, instead of 8-byte pieces scattered over 32 rows. `stage` is 8 KiB of
+// LDS that no other wave touches any more.
+template <typename T>
+__device__ __forceinline__ void store_rows_staged(const AttnArgs& a, const WgCoord& c, int wave,
+                                                  int lane, const f32x16 (&o)[4], float m_run,
+                                                  float l_run, unsigned char* stage) {
+    typedef __attribute__((ext_vector_type(4))) T t4;
+    const int lq = lane & 31;
+    const int hh = lane >> 5;
+    const int q0 = c.qb * kBlockQ + wave * 32;
+    const float inv_l = 1.0f / l_run;
+    unsigned char* wrow = stage + lq * 256;
+#pragma unroll
+    for (int nb = 0; nb < 4; ++nb) {
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            const t4 w = {(T)(o[nb][4 * g + 0] * inv_l), (T)(o[nb][4 * g + 1] * inv_l),
+                          (T)(o[nb][4 * g + 2] * inv_l), (T)(o[nb][4 * g + 3] * inv_l)};
+            const int pc = (4 * nb + g) ^ (lq & 15);
+            *reinterpret_cast<t4*>(wrow + 16 * pc + 8 * hh) = w;
+        }
+    }
+    const bool split = a.splits > 1;
+    const long slab = (long)c.split * a.frames + c.frame;
+    T* base = split ? static_cast<T*>(a.part_o) + slab * a.nq * (long)a.D
+                    : reinterpret_cast<T*>(a.out) + (long)c.frame * a.q_fstride;
+    base += c.head * kHeadDim;
+    const int lc = lane & 15;
+#pragma unroll
+    for (int it = 0; it < 8; ++it) {
+        const int row = 4 * it + (lane >> 4);
+        const u32x4 v = *reinterpret_cast<const u32x4*>(stage + row * 256 + 16 * (lc ^ (row & 15)));
+        const int q = q0 + row;
+        if (q < a.nq) *reinterpret_cast<u32x4*>(base + (long)q * a.D + 8 * lc) = v;
+    }
+    const int q = q0 + lq;
+    if (split && hh == 0 && q < a.nq)
+        a.part_lse[(slab * a.heads + c.head) * (long)a.nq + q] = m_run + __log2f(l_run);
 }
 
 // kMap: the launch reads a KVMap (a.kvmap != null); the map-free variant has
@@ -685,7 +698,15 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_bf16_kernel(AttnArgs a) 
     // the trailing copies land before the workgroup's LDS is released
     wait_vm<0>();
 
-    store_rows<OutT>(a, c, q, hh, o, m_run, l_run);
+    // Stage in the last tile's stage: every wave has passed the barrier that
+    // closed its last read, and the trailing copies target the other stage.
+    unsigned char* last_k = (ntiles > 0 && ((ntiles - 1) & 1)) ? k_lds1 : k_lds0;
+    unsigned char* last_v = (ntiles > 0 && ((ntiles - 1) & 1)) ? v_lds1 : v_lds0;
+    unsigned char* stage = (wave < 2 ? last_k : last_v) + 8192 * (wave & 1);
+    if (a.splits > 1)
+        store_rows_staged<_Float16>(a, c, wave, lane, o, m_run, l_run, stage);
+    else
+        store_rows_staged<OutT>(a, c, wave, lane, o, m_run, l_run, stage);
 }
 
 // ---------------------------------------------------------------------------
@@ -812,7 +833,7 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_f32_kernel(AttnArgs a) {
         __syncthreads();
     }
 
-    store_rows<float>(a, c, q, hh, o, m_run, l_run);
+    store_rows_f32(a, c, q, hh, o, m_run, l_run);
 }
 
 // ---------------------------------------------------------------------------
@@ -839,9 +860,21 @@ __device__ __forceinline__ void combine_block(const AttnArgs& a, long block) {
         if (s < a.splits) {
             const long slab = (long)s * a.frames + frame;
             lse[s] = a.part_lse[(slab * a.heads + head) * (long)a.nq + q];
-            const float* po = a.part_o + (slab * a.nq + q) * (long)a.D + 8 * c8;
-            p0[s] = *reinterpret_cast<const f32x4*>(po);
-            p1[s] = *reinterpret_cast<const f32x4*>(po + 4);
+            const long pofs = (slab * a.nq + q) * (long)a.D + 8 * c8;
+            if constexpr (sizeof(OutT) == 4) {
+                const float* po = static_cast<const float*>(a.part_o) + pofs;
+                p0[s] = *reinterpret_cast<const f32x4*>(po);
+                p1[s] = *reinterpret_cast<const f32x4*>(po + 4);
+            } else {
+                typedef __attribute__((ext_vector_type(8))) _Float16 f16x8;
+                const f16x8 h =
+                    *reinterpret_cast<const f16x8*>(static_cast<const _Float16*>(a.part_o) + pofs);
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    p0[s][i] = (float)h[i];
+                    p1[s][i] = (float)h[4 + i];
+                }
+            }
         }
     }
     float mx = lse[0];
@@ -1118,14 +1151,14 @@ int launch_attention(int dtype, const void* q, const void* k, const void* v, con
     a.scale_log2 = kLog2e / sqrtf((float)kHeadDim);
 
     if (p.splits > 1) {
-        const size_t po = (size_t)p.splits * frames * nq * D * sizeof(float);
+        const size_t po = (size_t)p.splits * frames * nq * D * (dtype == 1 ? 2 : 4);
         const size_t pl = (size_t)p.splits * frames * heads * nq * sizeof(float);
         char* ws = static_cast<char*>(workspace(dev, po + pl + 256));
         if (!ws) {
             set_error("attention: workspace allocation of %zu bytes failed", po + pl);
             return 1;
         }
-        a.part_o = reinterpret_cast<float*>(ws);
+        a.part_o = ws;
         a.part_lse = reinterpret_cast<float*>(ws + ((po + 255) / 256) * 256);
     }
     if (p.grid > 0x7fffffffL) {
