@@ -373,9 +373,8 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_bf16_kernel(AttnArgs a) 
 #pragma unroll
         for (int ks = 0; ks < 8; ++ks)
             qf[ks] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(qp + 16 * ks));
-        // Resolve the Q loads before the copy pipeline starts, so the loop
-        // never waits for vector memory on their account.
-        __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
+        // The Q loads stay in flight while the KVMap words and the first
+        // tile's copies are issued; one wait below covers them all.
     }
 
     // Copy assignment: instruction i of wave w fills LDS bytes [(4w+i)*1 KiB, +1 KiB)
@@ -665,6 +664,9 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_bf16_kernel(AttnArgs a) 
 #pragma unroll
         for (int i = 0; i < 4; ++i) copy_pair(i);
     }
+    // Compiler-visible wait for every load so far (Q, map, tile 0): the loop
+    // then never waits for vector memory on the Q registers' account.
+    __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
     for (int t = 0; t < ntiles; ++t) {
         // tile t lives in stage t & 1; tile t+1 streams into the other stage,
         // which every wave finished reading before the barrier that closed
