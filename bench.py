@@ -1,7 +1,7 @@
 #!/usr/bin/env python3
 """Benchmark of the KVMap-attention + KV-arena hot path on one MI355X.
 
-Workload ("C3"): Wan2.1-1.3B attention shape,
+Workload "C3", the configuration of the headline metric: Wan2.1-1.3B shape,
 8 frames x 1560 tokens, 12 heads x 128, 30 layers, bf16 Q/K/V ~ N(0,1)
 (drawn on the device, seed 42 + layer), causal cross-frame attention, motion
 scores from a seeded smooth AR(1) field. One step = the whole 30-layer pass:

@@ -3,7 +3,7 @@
 Restates the reference's variance study (reference: tests/test_variance.py:1-240)
 on MI355X with rocprofv3 counters instead of Nsight Compute:
 
-* workload: BASELINE config C4 — 50 query frames of 1560 tokens, causal
+* workload: C4 — 50 query frames of 1560 tokens, causal
   cross-frame attention over a sliding window of 8 frames, 12 heads x 128,
   bf16, one layer (the reference's `policy_experiment` also runs one
   attention launch per frame), synthetic device N(0,1) Q/K/V and the C4

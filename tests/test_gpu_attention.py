@@ -1,6 +1,6 @@
 """GPU parity of the attention kernels against the CPU oracle.
 
-Tolerances (BASELINE north star): fp32 max-abs <= 1e-3 and mean-abs <= 1e-4
+Tolerances: fp32 max-abs <= 1e-3 and mean-abs <= 1e-4
 against the fp32 golden (reference: tests/test_correctness.py:26-27);
 bf16 max-abs <= 2e-2 against the fp32 golden of bf16-rounded inputs.
 KVMap indirection must not change a single bit of the output.
