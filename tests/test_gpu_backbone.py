@@ -329,3 +329,41 @@ def test_produced_kv_feed_the_arena_pipeline():
     want = at.attention_frames(ql.float().cpu(), kl.float().cpu(), vl.float().cpu(), frames, T,
                                heads, "cross")
     assert float((outs["none"].float() - want).abs().max()) <= BF16_MAX
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("dtype", [0, 1])
+def test_backbone_forward_layouts_and_growth(dtype):
+    """C-ABI forward with a layer stride larger than one layer's K/V (the gap
+    is untouched), q_out NULL, a second call with more frames (scratch grows)
+    and one head (D = 128: the 128-feature projection tile) — K/V equal the
+    token-major forward of the Python mirror bit for bit."""
+    cfg = _cfg(2, 64, 1)
+    model = kb.SelfAttentionBackbone(cfg, seed=31, dtype=dtype)
+    lib = _lib.load()
+    D, T, L = cfg.hidden_dim, cfg.tokens_per_frame, cfg.num_layers
+    rng = np.random.default_rng(32)
+    dt = TDT[dtype]
+    for frames in (1, 3):
+        lat = torch.from_numpy(rng.standard_normal((frames, 16, 8, 8)).astype(np.float32)).to(DEV)
+        rows = frames * T
+        stride = rows * D + 256
+        sentinel = -7.0
+        k = torch.full((L * stride,), sentinel, dtype=dt, device=DEV)
+        v = torch.full((L * stride,), sentinel, dtype=dt, device=DEV)
+        assert lib.kvp_backbone_forward(model._h, lat.data_ptr(), frames, None, None,
+                                        k.data_ptr(), v.data_ptr(), stride, None) == 0, \
+            _lib.last_error()
+        _, k_ref, v_ref, _ = model.forward_token_major(lat)
+        torch.cuda.synchronize()
+        for l in range(L):
+            seg_k = k[l * stride:(l + 1) * stride]
+            seg_v = v[l * stride:(l + 1) * stride]
+            assert torch.equal(seg_k[:rows * D].view(rows, D), k_ref[l])
+            assert torch.equal(seg_v[:rows * D].view(rows, D), v_ref[l])
+            assert bool((seg_k[rows * D:] == sentinel).all()) and bool(
+                (seg_v[rows * D:] == sentinel).all())
+    # a stride that breaks 16-byte alignment is refused before any launch
+    assert lib.kvp_backbone_forward(model._h, lat.data_ptr(), 3, None, None, k.data_ptr(),
+                                    v.data_ptr(), 3 * T * D + 1, None) != 0
+    assert "layer_stride" in _lib.last_error()
