@@ -162,7 +162,7 @@ def producer_bench(args, torch, stream):
             # the three row blocks of qkv_proj in one grouped launch, as the
             # backbone runs them
             kb.proj_gemm(xn, P[b + "attn.qkv_proj.weight"], P[b + "attn.qkv_proj.bias"],
-                         [q, k, v], tile_n=256, stream=stream)
+                         [q, k, v], tile_n=128, stream=stream)
             marks[2].record()
             api.attn_forward_launcher_bf16(q, k, v, None, None, ctx, frames, T, D, H,
                                            remap=False)

@@ -457,8 +457,7 @@ int qkv_project_impl(int dtype, const float* x, const float* ln_w, const float* 
     if (dtype == 1) {
         // bf16: one launch of the grouped projection kernel writes q, k and v
         void* outs[3] = {q, k, v};
-        const int tile = D % 256 == 0 ? 256 : 128;
-        const int rc = launch_proj_gemm(xn, w_qkv, b_qkv, outs, 3, rows, D, D, 1, false, tile,
+        const int rc = launch_proj_gemm(xn, w_qkv, b_qkv, outs, 3, rows, D, D, 1, false, 128,
                                         stream);
         if (rc != 2) return rc;  // 2: shape outside the kernel's tiling, use hipBLASLt
         clear_error();

@@ -52,8 +52,9 @@ void stage_plan_free(void* plan);
 // Grouped bf16 projection GEMM (proj_gemm.hip): for g < groups (1..3),
 // outs[g][r, n] = sum_k x[r, k] w[g*Ng + n, k] + bias[g*Ng + n]
 // (+ outs[g][r, n] when accumulate; fp32 output only). x, w bf16; bias fp32
-// or null; out_dtype 0 = fp32, 1 = bf16; tile_n 128 or 256 features per
-// workgroup tile. Returns 0 on success, 2 when the shape is outside the
+// or null; out_dtype 0 = fp32, 1 = bf16; tile_n 128 (128 x 128 tiles, two
+// workgroups per CU) or 256 (256 x 256 tiles, one workgroup per CU).
+// Returns 0 on success, 2 when the shape is outside the
 // kernel's tiling (K % 64 or Ng % tile_n), 1 on any other error.
 int launch_proj_gemm(const void* x, const void* w, const float* bias, void* const* outs,
                      int groups, long rows, int K, int Ng, int out_dtype, bool accumulate,

@@ -10,7 +10,12 @@
 // three token-major outputs, and out_proj (src/backbone.py:22,32-33) adds
 // into the fp32 residual stream in its epilogue.
 //
-// Work decomposition:
+// Two tilings share the operand layout below: the large-tile kernel (256 x
+// 256, one workgroup per CU) and the small-tile kernel (128 x 128, two
+// workgroups per CU, described at its definition), which is the faster one
+// at the backbone's shapes and the one the q/k/v projection uses.
+//
+// Work decomposition (large tiles):
 //   workgroup = 4 waves, output tile TN features x 256 tokens; wave (wn, wr)
 //   owns (TN/2) x 128 of it as (TN/64) x 4 blocks of 32x32 accumulated by
 //   v_mfma_f32_32x32x16_bf16 with A = w rows (features), B = x rows
@@ -53,7 +58,8 @@ typedef __attribute__((ext_vector_type(16))) float f32x16;
 typedef __attribute__((ext_vector_type(4))) unsigned int u32x4;
 
 constexpr int kPThreads = 256;
-constexpr int kPTileR = 256;   // tokens per workgroup tile
+constexpr int kPTileR = 256;   // tokens per workgroup tile (large-tile kernel)
+constexpr int kPSmall = 128;   // features and tokens per tile (small-tile kernel)
 constexpr int kPChunkK = 64;   // K per LDS stage
 constexpr int kPRowBytes = kPChunkK * 2;
 constexpr int kPBand = 4;      // token tiles per scheduling band
@@ -341,11 +347,204 @@ __global__ __launch_bounds__(kPThreads, 1) void proj_gemm_bf16_kernel(ProjArgs a
     }
 }
 
-template <int TN, typename OutT, bool kAcc>
-void launch_tn(const ProjArgs& a, hipStream_t st) {
+// Small-tile form: TN features x TR tokens per workgroup (128 x 128), two
+// workgroups per CU (64 KiB of LDS each: K chunks of 64 in a two-stage ring,
+// the same 128-byte swizzled rows as above); wave (wn, wr) owns (TN/2) x
+// (TR/2) as (TN/64) x (TR/64) blocks. Each chunk's copies are issued right
+// after the barrier that frees their stage. With two resident workgroups the
+// one in its epilogue or waiting on copies leaves the MFMA pipe to the other,
+// and four times as many tiles even out the rounds over the CUs.
+template <int TN, int TR, typename OutT, bool kAcc>
+__global__ __launch_bounds__(kPThreads, 2) void proj_gemm_bf16_small_kernel(ProjArgs a) {
+    constexpr int JN = TN / 64, JR = TR / 64;
+    constexpr int kWB = TN * kPRowBytes, kXB = TR * kPRowBytes, kSB = kWB + kXB;
+    constexpr int kWC = kWB / 4096, kXC = kXB / 4096, kCP = kWC + kXC;  // copies per wave
+    __shared__ __attribute__((aligned(1024))) unsigned char lds[2 * kSB];
+
+    const int lid = pj_xcd_remap((int)blockIdx.x, (int)gridDim.x);
+    const int band_tiles = kPBand * a.n_tiles;
+    const int band = lid / band_tiles;
+    const int in_band = lid % band_tiles;
+    const int band_r0 = band * kPBand;
+    int band_h = a.r_tiles - band_r0;
+    if (band_h > kPBand) band_h = kPBand;
+    const int rt = band_r0 + in_band % band_h;
+    const int nt = in_band / band_h;
+    const int tiles_per_group = a.Ng / TN;
+    const int g = nt / tiles_per_group;
+    const int n0 = (nt % tiles_per_group) * TN;
+    const long r0 = (long)rt * TR;
+
+    const int tid = threadIdx.x;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int lane = tid & 63;
+    const int lq = lane & 31;
+    const int hh = lane >> 5;
+    const int wn = wave & 1;
+    const int wr = wave >> 1;
+
+    const unsigned kbytes = (unsigned)a.K * 2u;
+    long xrows = a.rows - r0;
+    if (xrows > TR) xrows = TR;
+    const __amdgpu_buffer_rsrc_t wrs = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<__bf16*>(a.w + ((long)g * a.Ng + n0) * a.K), (short)0, (int)(TN * kbytes),
+        kPBufFlags);
+    const __amdgpu_buffer_rsrc_t xrs = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<__bf16*>(a.x + r0 * a.K), (short)0, (int)(xrows * (long)kbytes), kPBufFlags);
+    const unsigned lds0 = (unsigned)(uintptr_t)lds;
+    // copy c of a chunk: 1 KiB block blk of the weight (c < kWC) or token
+    // operand, rows 8*blk + lane/8, physical chunk lane % 8
+    auto issue_copy = [&](int c, int stage, unsigned kofs) {
+        const bool isw = c < kWC;
+        const int blk = (isw ? kWC : kXC) * wave + (isw ? c : c - kWC);
+        const unsigned row = 8u * (unsigned)blk + (unsigned)(lane >> 3);
+        const unsigned lc = (unsigned)(lane & 7) ^ ((row >> 1) & 7u);
+        const unsigned dst = lds0 + (unsigned)(stage * kSB) + (isw ? 0u : (unsigned)kWB) +
+                             1024u * (unsigned)blk;
+        PJ_LDS void* d = (PJ_LDS void*)(uintptr_t)(unsigned)__builtin_amdgcn_readfirstlane((int)dst);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(isw ? wrs : xrs, d, 16, row * kbytes + 16u * lc,
+                                                 (int)kofs, 0, 0);
+    };
+    const unsigned fs = (unsigned)((lq >> 1) & 7);
+    const unsigned w_row = (unsigned)(wn * (TN / 2) + lq) * kPRowBytes;
+    const unsigned x_row = (unsigned)(wr * (TR / 2) + lq) * kPRowBytes;
+    constexpr int NF = JN + JR;
+    auto read_frags = [&](u32x4 (&f)[NF], int stage, int ks) {
+        const unsigned fo = ((unsigned)(2 * ks + hh) ^ fs) << 4;
+        const unsigned wa = lds0 + (unsigned)(stage * kSB) + w_row + fo;
+        const unsigned xa = lds0 + (unsigned)(stage * kSB + kWB) + x_row + fo;
+        f[0] = pj_lds_b128<0>(wa);
+        if constexpr (JN > 1) f[1] = pj_lds_b128<32 * kPRowBytes>(wa);
+        f[JN] = pj_lds_b128<0>(xa);
+        if constexpr (JR > 1) f[JN + 1] = pj_lds_b128<32 * kPRowBytes>(xa);
+    };
+    static_assert(JN <= 2 && JR <= 2, "fragment reads cover two blocks per operand");
+
+    f32x16 acc[JN][JR];
+    {
+        const float* bias = a.bias ? a.bias + (long)g * a.Ng + n0 + wn * (TN / 2) : nullptr;
+#pragma unroll
+        for (int i = 0; i < JN; ++i) {
+#pragma unroll
+            for (int q4 = 0; q4 < 4; ++q4) {
+                const float4 b4 = bias ? *reinterpret_cast<const float4*>(bias + 32 * i + 8 * q4 +
+                                                                          4 * hh)
+                                       : make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+                for (int j = 0; j < JR; ++j) {
+                    acc[i][j][4 * q4 + 0] = b4.x;
+                    acc[i][j][4 * q4 + 1] = b4.y;
+                    acc[i][j][4 * q4 + 2] = b4.z;
+                    acc[i][j][4 * q4 + 3] = b4.w;
+                }
+            }
+        }
+    }
+
+    const int nk = a.K / kPChunkK;
+#pragma unroll
+    for (int c = 0; c < kCP; ++c) issue_copy(c, 0, 0u);
+    u32x4 fr[2][NF];
+    for (int t = 0; t < nk; ++t) {
+        const int st = t & 1;
+        // chunk t has landed for every wave after the barrier, and every
+        // wave has finished chunk t-1, whose stage the next copies refill
+        pj_wait_vm0();
+        pj_barrier();
+        if (t + 1 < nk) {
+#pragma unroll
+            for (int c = 0; c < kCP; ++c) issue_copy(c, st ^ 1, (unsigned)(t + 1) * kPRowBytes);
+        }
+        read_frags(fr[0], st, 0);
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks) {
+            u32x4 (&cur)[NF] = fr[ks & 1];
+            pj_lgkm_wait(cur);
+            if (ks < 3) read_frags(fr[(ks + 1) & 1], st, ks + 1);
+            __builtin_amdgcn_s_setprio(1);
+#pragma unroll
+            for (int i = 0; i < JN; ++i)
+#pragma unroll
+                for (int j = 0; j < JR; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+                        __builtin_bit_cast(bf16x8, cur[i]), __builtin_bit_cast(bf16x8, cur[JN + j]),
+                        acc[i][j], 0, 0, 0);
+            __builtin_amdgcn_s_setprio(0);
+        }
+    }
+
+    // epilogue: as in the large-tile kernel, 32 tokens at a time
+    constexpr int kFeat = TN / 2;
+    constexpr int kEs = (int)sizeof(OutT);
+    constexpr int kRowB = kFeat * kEs + 16;
+    constexpr int kChunks = kFeat * kEs / 16;
+    constexpr int kRowsPerPass = 64 / kChunks;
+    static_assert(4 * 32 * kRowB <= 2 * kSB, "staging exceeds LDS");
+    pj_barrier();
+    OutT* out = static_cast<OutT*>(a.out[g]);
+    unsigned char* sbase = lds + wave * 32 * kRowB;
+    const int rchunk = lane % kChunks;
+    const int rrow = lane / kChunks;
+#pragma unroll
+    for (int j = 0; j < JR; ++j) {
+        unsigned char* wrow = sbase + lq * kRowB;
+#pragma unroll
+        for (int i = 0; i < JN; ++i) {
+#pragma unroll
+            for (int q4 = 0; q4 < 4; ++q4) {
+                const float v0 = acc[i][j][4 * q4 + 0];
+                const float v1 = acc[i][j][4 * q4 + 1];
+                const float v2 = acc[i][j][4 * q4 + 2];
+                const float v3 = acc[i][j][4 * q4 + 3];
+                OutT* p = reinterpret_cast<OutT*>(wrow) + 32 * i + 8 * q4 + 4 * hh;
+                if constexpr (kEs == 4) {
+                    *reinterpret_cast<float4*>(p) = make_float4(v0, v1, v2, v3);
+                } else {
+                    struct alignas(8) B4 {
+                        __bf16 v[4];
+                    } o;
+                    o.v[0] = (__bf16)v0;
+                    o.v[1] = (__bf16)v1;
+                    o.v[2] = (__bf16)v2;
+                    o.v[3] = (__bf16)v3;
+                    *reinterpret_cast<B4*>(p) = o;
+                }
+            }
+        }
+#pragma unroll
+        for (int pass = 0; pass < 32 / kRowsPerPass; ++pass) {
+            const int row = pass * kRowsPerPass + rrow;
+            const long r = r0 + wr * (TR / 2) + 32 * j + row;
+            const u32x4 vals = *reinterpret_cast<const u32x4*>(sbase + row * kRowB + 16 * rchunk);
+            if (r >= a.rows) continue;
+            unsigned char* gp = reinterpret_cast<unsigned char*>(out + r * a.Ng + n0 + wn * kFeat) +
+                                16 * rchunk;
+            if constexpr (kAcc) {
+                float4 y = *reinterpret_cast<const float4*>(gp);
+                y.x += __uint_as_float(vals[0]);
+                y.y += __uint_as_float(vals[1]);
+                y.z += __uint_as_float(vals[2]);
+                y.w += __uint_as_float(vals[3]);
+                *reinterpret_cast<float4*>(gp) = y;
+            } else {
+                *reinterpret_cast<u32x4*>(gp) = vals;
+            }
+        }
+    }
+}
+
+template <typename OutT, bool kAcc>
+void launch_large(const ProjArgs& a, hipStream_t st) {
     const int grid = a.n_tiles * a.r_tiles;
-    hipLaunchKernelGGL((proj_gemm_bf16_kernel<TN, OutT, kAcc>), dim3((unsigned)grid),
+    hipLaunchKernelGGL((proj_gemm_bf16_kernel<256, OutT, kAcc>), dim3((unsigned)grid),
                        dim3(kPThreads), 0, st, a);
+}
+
+template <typename OutT, bool kAcc>
+void launch_small(const ProjArgs& a, hipStream_t st) {
+    const int grid = a.n_tiles * a.r_tiles;
+    hipLaunchKernelGGL((proj_gemm_bf16_small_kernel<kPSmall, kPSmall, OutT, kAcc>),
+                       dim3((unsigned)grid), dim3(kPThreads), 0, st, a);
 }
 
 }  // namespace
@@ -385,7 +584,8 @@ int launch_proj_gemm(const void* x, const void* w, const float* bias, void* cons
         set_error("proj_gemm: operands must be 16-byte aligned");
         return 1;
     }
-    const long r_tiles = (rows + kPTileR - 1) / kPTileR;
+    const long tile_r = tile_n == 256 ? kPTileR : kPSmall;
+    const long r_tiles = (rows + tile_r - 1) / tile_r;
     const long n_tiles = (long)groups * (Ng / tile_n);
     if (r_tiles * n_tiles > 0x7fffffffL) {
         set_error("proj_gemm: grid too large");
@@ -405,18 +605,18 @@ int launch_proj_gemm(const void* x, const void* w, const float* bias, void* cons
     hipStream_t st = static_cast<hipStream_t>(stream);
     if (tile_n == 256) {
         if (out_dtype == 1)
-            launch_tn<256, __bf16, false>(a, st);
+            launch_large<__bf16, false>(a, st);
         else if (accumulate)
-            launch_tn<256, float, true>(a, st);
+            launch_large<float, true>(a, st);
         else
-            launch_tn<256, float, false>(a, st);
+            launch_large<float, false>(a, st);
     } else {
         if (out_dtype == 1)
-            launch_tn<128, __bf16, false>(a, st);
+            launch_small<__bf16, false>(a, st);
         else if (accumulate)
-            launch_tn<128, float, true>(a, st);
+            launch_small<float, true>(a, st);
         else
-            launch_tn<128, float, false>(a, st);
+            launch_small<float, false>(a, st);
     }
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) {

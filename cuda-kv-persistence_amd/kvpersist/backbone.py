@@ -96,7 +96,7 @@ def linear(x: torch.Tensor, weight, bias, out: torch.Tensor, accumulate: bool = 
     return out
 
 
-def proj_gemm(x: torch.Tensor, weight, bias, outs, accumulate: bool = False, tile_n: int = 256,
+def proj_gemm(x: torch.Tensor, weight, bias, outs, accumulate: bool = False, tile_n: int = 128,
               stream: int | None = None) -> None:
     """Grouped projection on the hand-written kernel: outs[g] (+)= x W_g^T + b_g
     with W_g the g-th [N]-row block of weight (bf16) and N = outs[0].shape[-1]."""

@@ -46,8 +46,9 @@ int kvp_linear(int in_dtype, int out_dtype, const void* x, const void* w,
  * all groups: the q/k/v row blocks of qkv_proj written to three outputs, or
  * out_proj added into the fp32 residual stream (reference:
  * src/backbone.py:13-14,18-22,32-33). K a multiple of 64, N a multiple of
- * tile_n (128 or 256 features per workgroup tile). Unused outputs may be
- * NULL. */
+ * tile_n: 128 = 128 x 128 tiles, two workgroups per CU (the faster form at
+ * the backbone's shapes); 256 = 256 x 256 tiles, one workgroup per CU.
+ * Unused outputs may be NULL. */
 int kvp_proj_gemm(const void* x, const void* w, const float* bias,
                   void* out0, void* out1, void* out2, int groups, long rows,
                   int K, int N, int out_dtype, int accumulate, int tile_n,

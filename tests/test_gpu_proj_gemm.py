@@ -35,6 +35,8 @@ CASES = [
     (1000, 1536, 1536, 1, 256, 0, True, True),
     (1560, 1536, 1536, 1, 128, 0, True, True),
     (12480, 1536, 1536, 3, 256, 1, False, True),
+    (12480, 1536, 1536, 3, 128, 1, False, True),
+    (12480, 1536, 1536, 1, 128, 0, True, True),
 ]
 
 
