@@ -70,7 +70,9 @@ int kvp_qkv_project(int dtype, const float* x, const float* ln_weight,
  * biases 0, LayerNorm weight 1 and bias 0; the normals come from this
  * library's own seeded generator (identical for equal seeds), not torch's.
  * The two projections of each block are stored in the model dtype, every
- * other parameter in fp32. Returns NULL on a bad config. */
+ * other parameter in fp32. Returns NULL on a bad config. An object runs one
+ * forward at a time (its activation scratch is shared between calls and
+ * grown, with a device synchronisation, when more frames arrive). */
 void* kvp_backbone_create(int dtype, int num_layers, int tokens_per_frame,
                           int hidden_dim, int num_heads, int latent_channels,
                           unsigned long seed);
