@@ -23,6 +23,7 @@ c_float_p = ctypes.POINTER(ctypes.c_float)
 c_long_p = ctypes.POINTER(ctypes.c_long)
 c_int_p = ctypes.POINTER(ctypes.c_int)
 c_size_t = ctypes.c_size_t
+c_double = ctypes.c_double
 
 # name -> (restype, argtypes); every symbol declared in include/*.h.
 SIGNATURES = {
@@ -142,6 +143,16 @@ SIGNATURES = {
     "kvp_backbone_get_param": (c_int, [c_void_p, c_char_p, c_float_p, c_long]),
     "kvp_backbone_forward": (c_int, [c_void_p, c_void_p, c_int, c_void_p, c_void_p, c_void_p,
                                      c_void_p, c_long, c_void_p]),
+    # upstream motion producer (reference: traces/gen_motion_from_video.py:61-67,104-126)
+    "kvp_farneback_workspace_bytes": (c_long, [c_int, c_int, c_int, c_double, c_int]),
+    "kvp_farneback_flows": (c_int, [c_void_p, c_int, c_int, c_int, c_double, c_int, c_int, c_int,
+                                    c_int, c_double, c_int, c_void_p, c_long, c_void_p,
+                                    c_void_p]),
+    "kvp_farneback_flow": (c_int, [c_void_p, c_void_p, c_void_p, c_int, c_int, c_double, c_int,
+                                   c_int, c_int, c_int, c_double, c_int, c_void_p, c_long,
+                                   c_void_p]),
+    "kvp_motion_change_rates": (c_int, [c_void_p, c_int, c_int, c_int, c_int, c_int, c_int,
+                                        c_void_p, c_void_p, c_void_p]),
 }
 
 _LIB = None

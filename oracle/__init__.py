@@ -21,6 +21,10 @@ Modules
   backbone    the upstream K/V producer: LayerNorm, the q/k/v projections,
               the DiT block and the backbone forward in float64
               (reference: src/backbone.py:8-67).
+  farneback   the upstream motion producer: OpenCV's Farneback dense flow
+              restated from its published algorithm, the per-tile change
+              rates and the trace post-processing
+              (reference: traces/gen_motion_from_video.py:61-149).
   ref_build   recipe compiling the reference's own policy source into
               oracle/_ref/ (this container only; never shipped).
 

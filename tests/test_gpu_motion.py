@@ -1,0 +1,163 @@
+"""GPU parity of the upstream motion producer (include/kvp_motion.h) against
+oracle/farneback.py, through the C-ABI.
+
+Tolerances (fp32 kernels with fp64 solves against the float64 oracle):
+flow |error| <= 1e-4 px at the 99.9th percentile, mean <= 5e-6 px, and max
+<= 5e-2 px. The max bound is loose on purpose: the update step branches on
+floor(x + dx) against the last row and column (bilinear sample or R0-only
+fallback), and where x + dx lands within rounding of that edge fp32 and the
+oracle may branch differently, a jump the box filter spreads over one
+window. Cell maps and tile change rates: within 1e-4 relative + 1e-5
+absolute of the oracle applied to the same flow. Size-independent
+properties are checked at the reference's full 832x480 size: a known
+translation is recovered, identical frames give exactly zero flow outside
+the far-border band, the pair entry point equals the clip entry point bit
+for bit.
+"""
+
+import numpy as np
+import pytest
+import torch
+from scipy import ndimage
+
+from kvpersist import motion
+from oracle import farneback as fb
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+FLOW_P999, FLOW_MEAN, FLOW_MAX = 1e-4, 5e-6, 5e-2
+
+
+def _texture(h, w, seed, sigma=2.5, pad=40):
+    rng = np.random.default_rng(seed)
+    t = ndimage.gaussian_filter(rng.standard_normal((h + 2 * pad, w + 2 * pad)), sigma,
+                                mode="wrap")
+    return (t - t.mean()) / t.std(), pad
+
+
+def _shifted(tex, pad, h, w, dx, dy):
+    yy, xx = np.mgrid[0:h, 0:w].astype(np.float64)
+    img = ndimage.map_coordinates(tex, [yy + pad - dy, xx + pad - dx], order=3, mode="wrap")
+    return np.clip(np.rint(128 + 40 * img), 0, 255).astype(np.uint8)
+
+
+def _flow_ok(got, want, what=""):
+    e = np.abs(np.asarray(got, np.float64) - np.asarray(want, np.float64))
+    mx, mean, p999 = float(e.max()), float(e.mean()), float(np.quantile(e, 0.999))
+    print(f"{what}: flow error max {mx:.3e} p99.9 {p999:.3e} mean {mean:.3e} px")
+    assert p999 <= FLOW_P999 and mean <= FLOW_MEAN and mx <= FLOW_MAX, (what, mx, p999, mean)
+
+
+@pytest.mark.parametrize("H,W,frames", [(96, 128, 3), (256, 320, 3), (480, 832, 3)])
+def test_clip_flows_match_oracle(H, W, frames):
+    clip = fb.synthetic_clip(frames, H, W, seed=H + W)
+    got = motion.farneback_flows(clip).cpu().numpy()
+    want = fb.farneback_clip(clip)
+    assert got.shape == want.shape == (frames - 1, H, W, 2)
+    _flow_ok(got, want, f"{H}x{W}")
+
+
+@pytest.mark.parametrize("params", [dict(levels=0), dict(winsize=9, iterations=2),
+                                    dict(poly_n=7, poly_sigma=1.5, pyr_scale=0.6, levels=2),
+                                    dict(iterations=0), dict(winsize=14)])
+def test_parameter_variants_match_oracle(params):
+    clip = fb.synthetic_clip(2, 128, 160, seed=7)
+    got = motion.calc_optical_flow_farneback(clip[0], clip[1], **params).cpu().numpy()
+    want = fb.calc_optical_flow_farneback(clip[0], clip[1], **params)
+    _flow_ok(got, want, str(params))
+
+
+def test_pair_entry_equals_clip_entry_bitwise():
+    clip = fb.synthetic_clip(4, 480, 832, seed=1)
+    flows = motion.farneback_flows(clip)
+    dev = torch.from_numpy(clip).to(DEV)
+    for p in range(3):
+        one = motion.calc_optical_flow_farneback(dev[p], dev[p + 1])
+        assert torch.equal(one, flows[p]), p
+
+
+@pytest.mark.parametrize("dx,dy", [(1.3, -0.7), (-6.5, 4.25)])
+def test_full_size_translation_is_recovered(dx, dy):
+    H, W = 480, 832
+    tex, pad = _texture(H, W, 3)
+    a, b = _shifted(tex, pad, H, W, 0, 0), _shifted(tex, pad, H, W, dx, dy)
+    flow = motion.calc_optical_flow_farneback(a, b).cpu().numpy()[24:-24, 24:-24]
+    assert abs(np.median(flow[..., 0]) - dx) < 0.05 and abs(np.median(flow[..., 1]) - dy) < 0.05
+    assert np.abs(flow[..., 0] - dx).mean() < 0.1 and np.abs(flow[..., 1] - dy).mean() < 0.1
+    # tile change rates of a pure translation: every interior tile near |(dx, dy)|
+    _, change = motion.change_rates(torch.from_numpy(
+        motion.calc_optical_flow_farneback(a, b).cpu().numpy()[None]).to(DEV))
+    mid = change.cpu().numpy()[0, 10:-10]
+    assert np.abs(np.median(mid) - np.hypot(dx, dy)) < 0.1
+
+
+def test_identical_frames_exact_zero_outside_far_band():
+    H, W = 480, 832
+    tex, pad = _texture(H, W, 4)
+    img = _shifted(tex, pad, H, W, 0, 0)
+    flow = motion.calc_optical_flow_farneback(img, img, levels=0).cpu().numpy()
+    band = 3 * 7 + 1
+    assert not flow[:H - band, :W - band].any()
+    assert flow[-1].any() and flow[:, -1].any()
+    _flow_ok(flow, fb.calc_optical_flow_farneback(img, img, levels=0), "identical frames")
+
+
+def test_change_rates_match_oracle():
+    rng = np.random.default_rng(5)
+    flows = (rng.standard_normal((3, 480, 832, 2)) * 2).astype(np.float32)
+    cells, change = motion.change_rates(torch.from_numpy(flows).to(DEV), 30, 52, 16)
+    cm_o, ch_o = fb.change_rates(flows, 30, 52, 16)
+    cells, change = cells.cpu().numpy(), change.cpu().numpy()
+    assert change.dtype == np.float64 and change.shape == (3, 98)
+    assert np.all(np.abs(cells - cm_o) <= 1e-4 * np.abs(cm_o) + 1e-5)
+    assert np.all(np.abs(change - ch_o) <= 1e-4 * np.abs(ch_o) + 1e-5)
+    # other grids and a tile size that leaves a short last tile
+    cells, change = motion.change_rates(torch.from_numpy(flows[:1]).to(DEV), 15, 26, 7)
+    cm_o, ch_o = fb.change_rates(flows[:1], 15, 26, 7)
+    assert change.shape == (1, -(-390 // 7))
+    assert np.all(np.abs(change.cpu().numpy() - ch_o) <= 1e-4 * np.abs(ch_o) + 1e-5)
+
+
+def test_motion_trace_matches_oracle_post_processing(tmp_path):
+    clip = fb.synthetic_clip(5, 480, 832, seed=9)
+    tr = motion.motion_trace(clip)
+    flows = motion.farneback_flows(clip).cpu().numpy()
+    _, pairs = fb.change_rates(flows, 30, 52, 16)
+    change, tau, reuse = fb.trace_from_change(pairs, 50.0)
+    assert tr.change.shape == (5, 98)
+    assert np.all(np.abs(tr.change - change) <= 1e-4 * np.abs(change) + 1e-5)
+    assert abs(tr.tau - tau) <= 1e-4 * abs(tau) + 1e-5
+    assert not tr.reuse[0].any() and abs(tr.reuse[1:].mean() - 0.5) < 0.01
+    csv_path, meta_path = motion.write_trace(tr, tmp_path, source="synthetic")
+    lines = csv_path.read_text().splitlines()
+    assert lines[0] == "frame_id,tile_id,motion_score,is_static,token_start,token_count,reuse"
+    assert len(lines) == 1 + 5 * 98
+    assert lines[98].split(",")[4:6] == ["1552", "8"]
+    import json
+    meta = json.loads(meta_path.read_text())
+    assert meta["num_tiles"] == 98 and meta["grid"] == [30, 52] and meta["cell_px"] == [16, 16]
+    assert meta["farneback"] == motion.FARNEBACK
+
+
+def test_bad_arguments_raise():
+    clip = fb.synthetic_clip(2, 64, 64, seed=2)
+    with pytest.raises(RuntimeError, match="flags"):
+        motion.calc_optical_flow_farneback(clip[0], clip[1], flags=256)
+    with pytest.raises(RuntimeError, match="winsize"):
+        motion.calc_optical_flow_farneback(clip[0], clip[1], winsize=61)
+    with pytest.raises(RuntimeError, match="poly_n"):
+        motion.calc_optical_flow_farneback(clip[0], clip[1], poly_n=9)
+    with pytest.raises(ValueError):
+        motion.calc_optical_flow_farneback(clip[0], clip[1], pyr_scale=1.0)
+    with pytest.raises(RuntimeError, match="grid"):
+        motion.change_rates(torch.zeros(1, 64, 64, 2, device=DEV), 30, 52, 16)
+    with pytest.raises(ValueError):
+        motion.motion_trace(clip)                       # fewer than 3 frames
+    from kvpersist import _lib
+    lib = _lib.load()
+    ws = torch.empty(16, dtype=torch.uint8, device=DEV)
+    f = torch.from_numpy(clip).to(DEV)
+    out = torch.empty(1, 64, 64, 2, device=DEV)
+    rc = lib.kvp_farneback_flows(f.data_ptr(), 2, 64, 64, 0.5, 3, 15, 3, 5, 1.2, 0,
+                                 ws.data_ptr(), 16, out.data_ptr(), None)
+    assert rc != 0 and "workspace" in _lib.last_error()
