@@ -17,7 +17,11 @@ same workload on this host's cores.
 
 Also reported under "kv_producer": the upstream K/V producer (the reference's
 DiT backbone forward, src/backbone.py:8-67) at the C3 frame set, whole
-forward and per stage, each stage against its roofline.
+forward and per stage, each stage against its roofline. Under
+"motion_producer": the upstream motion producer (the reference's Farneback
+flow + per-tile change rates, traces/gen_motion_from_video.py:104-121) over a
+50-frame 832x480 clip, per launch kind, the dominant kernel against the HBM
+roofline.
 
 python bench.py [--steps K] [--warmup W] [--policy P] [--layers L]
 """
@@ -61,6 +65,12 @@ def parse():
                     help="skip the upstream K/V producer measurement")
     ap.add_argument("--producer-only", action="store_true",
                     help="measure only the upstream K/V producer (prints its object) and exit")
+    ap.add_argument("--no-motion", action="store_true",
+                    help="skip the upstream motion producer measurement")
+    ap.add_argument("--motion-only", action="store_true",
+                    help="measure only the upstream motion producer (prints its object) and exit")
+    ap.add_argument("--motion-frames", type=int, default=50,
+                    help="clip length of the motion producer measurement")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="run 4 device-to-device copies of 256 MiB and exit (known-size "
                          "reference for FETCH_SIZE / WRITE_SIZE scaling)")
@@ -248,6 +258,116 @@ def producer_cpu_baseline(model, cfg, frames, layers):
                       f"1 layer, median of 3, x {layers} layers"}
 
 
+# Algorithmic HBM bytes per pixel of one full-size (level 0) launch, per frame
+# (pyramid kinds) or per pair (flow kinds); fp32 planes, uint8 frames.
+MOTION_BYTES_PER_PX = {
+    "blur_rows": 1 + 4,               # uint8 frame in, fp32 row-blurred out
+    "blur_cols_resize": 4 + 4,        # fp32 in, fp32 level image out
+    "poly_exp": 4 + 5 * 4,            # image in, 5 expansion planes out
+    "matrices_init": 2 + 5 * 4 * 2 + 5 * 4,  # coarse flow (1/4 px), R0 + R1, M out
+    "box_flow": 5 * 4 + 2 * 4,        # M in, flow out
+    "matrices": 2 * 4 + 5 * 4 * 2 + 5 * 4,   # flow, R0 + R1, M out
+}
+MOTION_PER_FRAME = ("blur_rows", "blur_cols_resize", "poly_exp")
+
+
+def motion_bench(args, torch, stream):
+    """Upstream motion producer (reference: traces/gen_motion_from_video.py:
+    104-121) over a synthetic clip resident in HBM: --motion-frames uint8 gray
+    frames of 832 x 480, Farneback(pyr_scale 0.5, levels 3, winsize 15,
+    iterations 3, poly_n 5, poly_sigma 1.2) for every consecutive pair, then
+    the 30 x 52 cell means and the 98 tile change rates per pair.
+
+    Whole clip: W warmup, K timed runs (HIP events on the launch stream).
+    Per launch: one run of kvp_farneback_profile (an event after every
+    launch); the kind with the most time at level 0 is the dominant kernel,
+    its achieved bandwidth = algorithmic bytes of one level-0 launch / its
+    average level-0 duration."""
+    from kvpersist import motion, workloads
+
+    n, H, W = args.motion_frames, 480, 832
+    clip = torch.from_numpy(workloads.synthetic_clip(n, H, W, seed=0)).cuda()
+    flows = torch.empty(n - 1, H, W, 2, device="cuda")
+    torch.cuda.synchronize()
+
+    def run():
+        motion.farneback_flows(clip, flows, stream=stream)
+        return motion.change_rates(flows, 30, 52, 16, stream=stream)
+
+    for _ in range(max(1, args.warmup)):
+        run()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(args.steps):
+        cells, change = run()
+    e1.record()
+    torch.cuda.synchronize()
+    clip_ms = e0.elapsed_time(e1) / args.steps
+    finite = bool(torch.isfinite(change).all())
+
+    _, launches = motion.farneback_profile(clip, flows, stream=stream)
+    per_kind, lvl0 = {}, {}
+    for kind, level, ms in launches:
+        per_kind[kind] = per_kind.get(kind, 0.0) + ms
+        if level == 0:
+            lvl0.setdefault(kind, []).append(ms)
+    dominant = max(lvl0, key=lambda k: sum(lvl0[k]))
+    P, pairs = H * W, n - 1
+
+    def level0_roof(kind):
+        units = n if kind in MOTION_PER_FRAME else pairs
+        nbytes = MOTION_BYTES_PER_PX[kind] * P * units
+        ms = sum(lvl0[kind]) / len(lvl0[kind])
+        ach = nbytes / (ms * 1e-3) / 1e9
+        return {"bound": "hbm", "achieved": round(ach, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": round(ach / HBM_PEAK_GBS, 4), "avg_launch_ms": round(ms, 5),
+                "launches_per_clip": len(lvl0[kind]),
+                "bytes_per_launch": nbytes,
+                "per_launch": f"{MOTION_BYTES_PER_PX[kind]} B/px x {P} px x {units} "
+                              f"{'frames' if kind in MOTION_PER_FRAME else 'pairs'}"}
+
+    out = {
+        "metric": "motion producer ms per frame pair (Farneback flow + tile change rates)",
+        "value": round(clip_ms / pairs, 5),
+        "unit": "ms/pair",
+        "higher_is_better": False,
+        "ms_per_clip": round(clip_ms, 4),
+        "pairs_per_s": round(pairs / (clip_ms * 1e-3), 1),
+        "outputs_finite": finite,
+        "config": {"workload": f"{n}-frame synthetic uint8 clip 832x480 (smooth texture, random "
+                               f"global shift + local warp), Farneback(0.5, 3, 15, 3, 5, 1.2, 0) "
+                               f"for all {pairs} pairs, 30x52 cells, 98 tiles of 16",
+                   "frames": n, "dtype": "f32"},
+        "launch_ms_per_clip": {k: round(v, 4) for k, v in per_kind.items()},
+        "launches_per_clip": len(launches),
+        "roofline": dict(level0_roof(dominant), kernel=dominant),
+        "level0_rooflines": {k: level0_roof(k) for k in lvl0},
+    }
+    if not args.no_cpu_baseline:
+        out["cpu_baseline"] = motion_cpu_baseline(clip[:3].cpu().numpy())
+    return out
+
+
+def motion_cpu_baseline(frames):
+    """The oracle's Farneback (numpy, float64) on a 3-frame sample of the same
+    clip: both pairs, each frame's expansion computed once, as the library
+    does; ms per pair."""
+    sys.path.insert(0, str(ROOT))
+    from oracle import farneback as fb
+    times = []
+    for _ in range(3):
+        t0 = time.perf_counter()
+        flows = fb.farneback_clip(frames)
+        fb.change_rates(flows, 30, 52, 16)
+        times.append(time.perf_counter() - t0)
+    per_pair = sorted(times)[1] / (frames.shape[0] - 1)
+    return {"value": round(per_pair * 1e3, 2), "unit": "ms/pair", "cores": 1, "kind": "port",
+            "sample": f"oracle numpy Farneback + change rates, {frames.shape[0]} frames "
+                      f"({frames.shape[0] - 1} pairs) of the bench clip at 832x480, median of 3 "
+                      f"(the reference's cv2 path is not in this image)"}
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -270,6 +390,10 @@ def main():
             assert lib.kvp_memcpy_d2d(dst.data_ptr(), src.data_ptr(), nbytes, None) == 0
         torch.cuda.synchronize()
         print(json.dumps({"copy_calibration_bytes_per_copy": nbytes, "copies": 4}), flush=True)
+        return
+    if args.motion_only:
+        mot = motion_bench(args, torch, torch.cuda.current_stream().cuda_stream)
+        print(json.dumps({"motion_producer": mot}), flush=True)
         return
     if args.producer_only:
         prod = producer_bench(args, torch, torch.cuda.current_stream().cuda_stream)
@@ -418,6 +542,10 @@ def main():
         log("upstream K/V producer ...")
         prod = producer_bench(args, torch, stream)
         log(f"producer {prod['value']} ms/frame")
+    mot = None
+    if not args.no_motion:
+        mot = motion_bench(args, torch, stream)
+        log(f"motion producer {mot['value']} ms/pair")
 
     value = ms_step / F
     line = {
@@ -457,6 +585,7 @@ def main():
         "policies": policies,
         "wall_ms_per_step": round(wall_step, 3),
         "kv_producer": prod,
+        "motion_producer": mot,
     }
     print(json.dumps(line), flush=True)
     main_pl.close()

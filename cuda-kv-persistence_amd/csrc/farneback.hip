@@ -13,8 +13,9 @@
 // level and shared by the two pairs that use it.
 //
 //   blur_rows_kernel         Gaussian pre-blur, horizontal pass, reflect-101
-//                            border, uint8 -> fp32, one row segment per
-//                            workgroup staged in LDS.
+//                            border, uint8 -> fp32: one source row per
+//                            workgroup staged in LDS, computed only at the
+//                            columns the level's resize samples.
 //   blur_cols_resize_kernel  vertical pass fused with the bilinear resize to
 //                            the level size (half-pixel centres, clamped
 //                            edges): only the 2 x 2 samples each level pixel
@@ -32,8 +33,10 @@
 //                            (zero, or the coarser level's flow resized and
 //                            scaled by 1/pyr_scale).
 //   update_flow_kernel       winsize x winsize box average of those 5 planes
-//                            (replicated border) and the regularised 2 x 2
-//                            solve in fp64; 64 x 16 tile + halo in LDS.
+//                            (replicated border): fp64 running column sums
+//                            slid down a strip of rows, parked in LDS 4 rows
+//                            at a time, sliding sums along runs of 2 columns;
+//                            then the regularised 2 x 2 solve in fp64.
 //   flow_cells_kernel        |flow| averaged over grid cells (one workgroup
 //                            per cell row), then tile_change_kernel: the mean
 //                            of each run of tile_tokens cells in fp64.
@@ -45,6 +48,7 @@
 
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cfloat>
 #include <cmath>
 #include <cstdint>
@@ -64,9 +68,10 @@ constexpr int kBorder = 5;          // down-weighted border width
 constexpr int kMinSide = 2 * kBorder;
 constexpr int kMaxSide = 8192;
 constexpr int kMaxFrames = 4096;
-constexpr int kRowSeg = 256;
 constexpr int kPeTileW = 64, kPeTileH = 16;
-constexpr int kUfTileW = 64, kUfTileH = 16;
+constexpr int kBfBatch = 4;       // box filter: rows parked in LDS at a time
+constexpr int kBfRun = 2;         // box filter: output columns per sliding run
+constexpr int kBfTargetGroups = 2048;
 
 struct BlurTaps {
     int ksize;
@@ -103,36 +108,72 @@ __device__ __forceinline__ void linear_tap(int d, double scale, int src, int& s0
     w = f;
 }
 
+// Horizontal pre-blur pass of one source row per workgroup, computed only at
+// the columns the level's resize samples: column j of the compact output is
+// source column tap(j / 2) + (j & 1) (both bilinear taps of level column
+// j / 2), or every column when the level has the source size. The row and its
+// reflect-101 halo are staged in LDS once.
 __global__ __launch_bounds__(256) void blur_rows_kernel(const uint8_t* __restrict__ src,
                                                         long frame_stride, int W, int H,
-                                                        float* __restrict__ out, BlurTaps t) {
-    __shared__ float row[kRowSeg + kMaxBlurTaps];
-    const int f = blockIdx.z, y = blockIdx.y, x0 = blockIdx.x * kRowSeg;
+                                                        float* __restrict__ out, int ncols,
+                                                        int same_size, double sx_scale,
+                                                        BlurTaps t) {
+    extern __shared__ float row[];
+    const int f = blockIdx.z, y = blockIdx.x;
     const uint8_t* s = src + (long)f * frame_stride + (long)y * W;
     const int h = t.ksize / 2;
-    const int span = kRowSeg + 2 * h;
-    for (int i = threadIdx.x; i < span; i += 256) row[i] = (float)s[reflect101(x0 - h + i, W)];
+    float* r = row + h;                      // r[-h .. W + h)
+    if ((W & 3) == 0 && (((uintptr_t)s) & 3) == 0) {
+        const uchar4* s4 = reinterpret_cast<const uchar4*>(s);
+        for (int i = threadIdx.x; i < W / 4; i += 256) {
+            const uchar4 v = s4[i];
+            r[4 * i] = v.x;
+            r[4 * i + 1] = v.y;
+            r[4 * i + 2] = v.z;
+            r[4 * i + 3] = v.w;
+        }
+    } else {
+        for (int i = threadIdx.x; i < W; i += 256) r[i] = s[i];
+    }
     __syncthreads();
-    const int x = x0 + threadIdx.x;
-    if (x >= W) return;
-    float acc = 0.f;
-    for (int j = 0; j < t.ksize; ++j) acc += t.k[j] * row[threadIdx.x + j];
-    out[((long)f * H + y) * W + x] = acc;
+    for (int i = threadIdx.x; i < 2 * h; i += 256) {
+        const int c = i < h ? i - h : W + (i - h);       // halo columns
+        r[c] = r[reflect101(c, W)];
+    }
+    __syncthreads();
+    float* o = out + ((long)f * H + y) * ncols;
+    for (int j = threadIdx.x; j < ncols; j += 256) {
+        int c;
+        if (same_size) {
+            c = j;
+        } else {
+            int c0, c1;
+            float wt;
+            linear_tap(j >> 1, sx_scale, W, c0, c1, wt);
+            c = (j & 1) ? c1 : c0;
+        }
+        float acc = 0.f;
+        for (int k = 0; k < t.ksize; ++k) acc += t.k[k] * r[c - h + k];
+        o[j] = acc;
+    }
 }
 
+// Vertical pre-blur pass fused with the bilinear resize: level pixel (x, y)
+// blends the vertically blurred compact columns 2x, 2x + 1 (or x at the
+// source size) at the two source rows its resize taps name.
 __global__ __launch_bounds__(256) void blur_cols_resize_kernel(
-        const float* __restrict__ hb, int W, int H, float* __restrict__ out, int w, int h,
-        double sx_scale, double sy_scale, int same_size, BlurTaps t) {
+        const float* __restrict__ hb, int ncols, int W, int H, float* __restrict__ out, int w,
+        int h, double sx_scale, double sy_scale, int same_size, BlurTaps t) {
     const int x = blockIdx.x * 64 + (threadIdx.x & 63);
     const int y = blockIdx.y * 4 + (threadIdx.x >> 6);
     const int f = blockIdx.z;
     if (x >= w || y >= h) return;
-    const float* base = hb + (long)f * H * W;
+    const float* base = hb + (long)f * H * ncols;
     const int hk = t.ksize / 2;
     auto col = [&](int r, int c) {
         float acc = 0.f;
         for (int j = 0; j < t.ksize; ++j)
-            acc += t.k[j] * base[(long)reflect101(r - hk + j, H) * W + c];
+            acc += t.k[j] * base[(long)reflect101(r - hk + j, H) * ncols + c];
         return acc;
     };
     float v;
@@ -143,8 +184,8 @@ __global__ __launch_bounds__(256) void blur_cols_resize_kernel(
         float wx, wy;
         linear_tap(x, sx_scale, W, xa, xb, wx);
         linear_tap(y, sy_scale, H, ya, yb, wy);
-        const float r0 = col(ya, xa) * (1.f - wx) + col(ya, xb) * wx;
-        const float r1 = col(yb, xa) * (1.f - wx) + col(yb, xb) * wx;
+        const float r0 = col(ya, 2 * x) * (1.f - wx) + col(ya, 2 * x + 1) * wx;
+        const float r1 = col(yb, 2 * x) * (1.f - wx) + col(yb, 2 * x + 1) * wx;
         v = r0 * (1.f - wy) + r1 * wy;
     }
     out[(long)f * w * h + (long)y * w + x] = v;
@@ -163,15 +204,14 @@ __global__ __launch_bounds__(256) void poly_exp_kernel(const float* __restrict__
     const long P = (long)w * h;
     const float* I = img + (long)f * P;
     const int tw = kPeTileW + 2 * n, th = kPeTileH + 2 * n;
-    for (int i = threadIdx.x; i < tw * th; i += 256) {
-        const int r = i / tw, c = i - r * tw;
-        const int yy = min(max(Y0 - n + r, 0), h - 1);
-        const int xx = min(max(X0 - n + c, 0), w - 1);
-        src[r * MW + c] = I[(long)yy * w + xx];
+    const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
+    for (int r = ty; r < th; r += 4) {
+        const float* Ir = I + (long)min(max(Y0 - n + r, 0), h - 1) * w;
+        for (int c = tx; c < tw; c += 64) src[r * MW + c] = Ir[min(max(X0 - n + c, 0), w - 1)];
     }
     __syncthreads();
-    for (int i = threadIdx.x; i < kPeTileH * tw; i += 256) {
-        const int r = i / tw, c = i - r * tw;
+    for (int r = ty; r < kPeTileH; r += 4)
+    for (int c = tx; c < tw; c += 64) {
         float s0 = src[(r + n) * MW + c] * t.g[n], s1 = 0.f, s2 = 0.f;
         for (int k = 1; k <= n; ++k) {
             const float lo = src[(r + n - k) * MW + c], hi = src[(r + n + k) * MW + c];
@@ -186,8 +226,8 @@ __global__ __launch_bounds__(256) void poly_exp_kernel(const float* __restrict__
     }
     __syncthreads();
     float* Rf = R + (long)f * 5 * P;
-    for (int i = threadIdx.x; i < kPeTileH * kPeTileW; i += 256) {
-        const int r = i / kPeTileW, c = i - r * kPeTileW;
+    for (int r = ty; r < kPeTileH; r += 4) {
+        const int c = tx;
         const int x = X0 + c, y = Y0 + r;
         if (x >= w || y >= h) continue;
         const float* v0 = &vp[0][r * MW + c + n];
@@ -307,51 +347,84 @@ __global__ __launch_bounds__(256) void update_matrices_kernel(
     Mp[4 * P] = r6 * r2 + r5 * r3;
 }
 
-__global__ __launch_bounds__(256) void update_flow_kernel(const float* __restrict__ M, int w,
-                                                          int h, int m, double scale,
-                                                          float2* __restrict__ flow) {
-    extern __shared__ float lds[];
-    const int tw = kUfTileW + 2 * m, th = kUfTileH + 2 * m;
-    float* tile = lds;
-    float* vs = lds + th * tw;
+// One workgroup = a strip of COLS - 2m output columns (COLS loaded columns
+// with the halo, one thread each) and `rows` output rows. Each thread keeps
+// fp64 running vertical sums of the 5 planes for its column (the entering
+// row added, the leaving row subtracted, replicated border) and parks them
+// in LDS for kBfBatch rows at a time; then each thread turns a run of
+// kBfRun columns of one parked row into box sums with a sliding horizontal
+// sum and solves those pixels.
+template <int COLS>
+__global__ __launch_bounds__(COLS) void update_flow_kernel(const float* __restrict__ M, int w,
+                                                           int h, int m, int rows, double scale,
+                                                           float2* __restrict__ flow) {
+    __shared__ float buf[kBfBatch][5][COLS];
+    const int tw = COLS - 2 * m;
+    const int X0 = blockIdx.x * tw;
+    const int Y0 = blockIdx.y * rows;
     const int p = blockIdx.z;
     const long P = (long)w * h;
-    const int X0 = blockIdx.x * kUfTileW, Y0 = blockIdx.y * kUfTileH;
     const float* Mp = M + (long)p * 5 * P;
-    for (int c = 0; c < 5; ++c) {
-        const float* Mc = Mp + c * P;
-        for (int i = threadIdx.x; i < th * tw; i += 256) {
-            const int r = i / tw, cc = i - r * tw;
-            const int yy = min(max(Y0 - m + r, 0), h - 1);
-            const int xx = min(max(X0 - m + cc, 0), w - 1);
-            tile[i] = Mc[(long)yy * w + xx];
-        }
-        __syncthreads();
-        for (int i = threadIdx.x; i < kUfTileH * tw; i += 256) {
-            const int r = i / tw, cc = i - r * tw;
-            float s = 0.f;
-            for (int k = 0; k <= 2 * m; ++k) s += tile[(r + k) * tw + cc];
-            vs[(c * kUfTileH + r) * tw + cc] = s;
-        }
-        __syncthreads();
-    }
-    for (int i = threadIdx.x; i < kUfTileH * kUfTileW; i += 256) {
-        const int r = i / kUfTileW, cc = i - r * kUfTileW;
-        const int x = X0 + cc, y = Y0 + r;
-        if (x >= w || y >= h) continue;
-        float s[5];
+    float2* Fp = flow + (long)p * P;
+    const int tid = threadIdx.x;
+    const int xc = min(max(X0 - m + tid, 0), w - 1);
+    double vs[5] = {0.0, 0.0, 0.0, 0.0, 0.0};
+    for (int r = Y0 - m; r <= Y0 + m; ++r) {
+        const float* q = Mp + (long)min(max(r, 0), h - 1) * w + xc;
 #pragma unroll
-        for (int c = 0; c < 5; ++c) {
-            const float* v = vs + (c * kUfTileH + r) * tw + cc;
-            float a = 0.f;
-            for (int k = 0; k <= 2 * m; ++k) a += v[k];
-            s[c] = a;
+        for (int c = 0; c < 5; ++c) vs[c] += q[c * P];
+    }
+    const int yend = min(Y0 + rows, h);
+    const int xend = min(tw, w - X0);                 // output columns of this strip
+    const int runs = (xend + kBfRun - 1) / kBfRun;
+    for (int yb = Y0; yb < yend; yb += kBfBatch) {
+        const int nr = min(kBfBatch, yend - yb);
+#pragma unroll
+        for (int r = 0; r < kBfBatch; ++r) {
+            if (r < nr) {
+#pragma unroll
+                for (int c = 0; c < 5; ++c) buf[r][c][tid] = (float)vs[c];
+                const int y = yb + r;
+                if (y + 1 < yend) {
+                    const float* qa = Mp + (long)min(y + m + 1, h - 1) * w + xc;
+                    const float* qs = Mp + (long)max(y - m, 0) * w + xc;
+#pragma unroll
+                    for (int c = 0; c < 5; ++c) vs[c] += (double)qa[c * P] - (double)qs[c * P];
+                }
+            }
         }
-        const double g11 = s[0] * scale, g12 = s[1] * scale, g22 = s[2] * scale;
-        const double h1 = s[3] * scale, h2 = s[4] * scale;
-        const double idet = 1.0 / (g11 * g22 - g12 * g12 + 1e-3);
-        flow[(long)p * P + (long)y * w + x] =
-            make_float2((float)((g11 * h2 - g12 * h1) * idet), (float)((g22 * h1 - g12 * h2) * idet));
+        __syncthreads();
+        for (int j = tid; j < nr * runs; j += COLS) {
+            const int r = j / runs;
+            const int x0 = (j - r * runs) * kBfRun;
+            const int n = min(kBfRun, xend - x0);
+            float s[5][kBfRun];
+#pragma unroll
+            for (int c = 0; c < 5; ++c) {
+                const float* v = &buf[r][c][x0];
+                float a = 0.f;
+                for (int k = 0; k <= 2 * m; ++k) a += v[k];
+                s[c][0] = a;
+#pragma unroll
+                for (int i = 1; i < kBfRun; ++i) {
+                    if (i < n) a += v[i + 2 * m] - v[i - 1];
+                    s[c][i] = a;
+                }
+            }
+            float2* out = Fp + (long)(yb + r) * w + X0 + x0;
+#pragma unroll
+            for (int i = 0; i < kBfRun; ++i) {
+                if (i < n) {
+                    const double g11 = s[0][i] * scale, g12 = s[1][i] * scale;
+                    const double g22 = s[2][i] * scale, h1 = s[3][i] * scale;
+                    const double h2 = s[4][i] * scale;
+                    const double idet = 1.0 / (g11 * g22 - g12 * g12 + 1e-3);
+                    out[i] = make_float2((float)((g11 * h2 - g12 * h1) * idet),
+                                         (float)((g22 * h1 - g12 * h2) * idet));
+                }
+            }
+        }
+        __syncthreads();
     }
 }
 
@@ -530,13 +603,16 @@ struct Layout {
 
 Layout layout(int nf, int W, int H, const std::vector<Level>& plan) {
     const size_t P0 = (size_t)W * H;
-    size_t P1 = 0;
+    size_t P1 = 0, hcols = W;   // row-blur output: W columns, or 2 per level column
     for (const Level& l : plan)
-        if (l.k > 0) P1 = std::max(P1, (size_t)l.w * l.h);
+        if (l.k > 0) {
+            P1 = std::max(P1, (size_t)l.w * l.h);
+            hcols = std::max(hcols, (size_t)2 * l.w);
+        }
     const size_t pairs = nf - 1;
     Layout L;
     size_t off = 0;
-    L.hbuf = off; off += align256(nf * P0 * sizeof(float));
+    L.hbuf = off; off += align256(nf * (size_t)H * hcols * sizeof(float));
     L.img = off;  off += align256(nf * P0 * sizeof(float));
     L.R = off;    off += align256(nf * 5 * P0 * sizeof(float));
     L.M = off;    off += align256(pairs * 5 * P0 * sizeof(float));
@@ -545,6 +621,16 @@ Layout layout(int nf, int W, int H, const std::vector<Level>& plan) {
     L.total = off;
     return L;
 }
+
+// launch kinds reported by kvp_farneback_profile
+enum {
+    KIND_BLUR_ROWS = 0,
+    KIND_BLUR_COLS_RESIZE = 1,
+    KIND_POLY_EXP = 2,
+    KIND_MATRICES_INIT = 3,
+    KIND_FLOW = 4,
+    KIND_MATRICES = 5,
+};
 
 int check_params(int nf, int W, int H, double pyr_scale, int levels, int winsize,
                  int iterations, int poly_n, int flags) {
@@ -580,10 +666,32 @@ int check_params(int nf, int W, int H, double pyr_scale, int levels, int winsize
     return 0;
 }
 
+// Launch timeline for kvp_farneback_profile: an event after every launch.
+struct Timeline {
+    hipStream_t st;
+    std::vector<hipEvent_t> ev;
+    std::vector<int> kind, level;
+    bool ok = true;
+    void mark(int k, int lv) {
+        hipEvent_t e;
+        if (hipEventCreate(&e) != hipSuccess) {
+            ok = false;
+            return;
+        }
+        if (hipEventRecord(e, st) != hipSuccess) ok = false;
+        ev.push_back(e);
+        kind.push_back(k);
+        level.push_back(lv);
+    }
+    ~Timeline() {
+        for (hipEvent_t e : ev) (void)hipEventDestroy(e);
+    }
+};
+
 int farneback_impl(const uint8_t* frames, long frame_stride, int nf, int W, int H,
                    double pyr_scale, int levels, int winsize, int iterations, int poly_n,
                    double poly_sigma, int flags, void* workspace, long workspace_bytes,
-                   float* flows, void* stream_v) {
+                   float* flows, void* stream_v, Timeline* tl = nullptr) {
     if (check_params(nf, W, H, pyr_scale, levels, winsize, iterations, poly_n, flags)) return 1;
     if (!frames || !flows || !workspace) {
         set_error("farneback: null pointer");
@@ -619,6 +727,10 @@ int farneback_impl(const uint8_t* frames, long frame_stride, int nf, int W, int 
     const int m = winsize / 2;
     const double box_scale = 1.0 / ((double)winsize * winsize);
 
+    auto mark = [&](int kind, int lv) {
+        if (tl) tl->mark(kind, lv);
+    };
+    mark(-1, -1);
     const float2* prev = nullptr;
     int pw = 0, ph = 0;
     for (size_t li = 0; li < plan.size(); ++li) {
@@ -626,14 +738,18 @@ int farneback_impl(const uint8_t* frames, long frame_stride, int nf, int W, int 
         BlurTaps bt;
         blur_taps(l.ksize, l.sigma, bt);
         const bool same = l.w == W && l.h == H;
-        blur_rows_kernel<<<dim3((W + kRowSeg - 1) / kRowSeg, H, nf), 256, 0, st>>>(
-            frames, frame_stride, W, H, hbuf, bt);
+        const int ncols = same ? W : 2 * l.w;
+        const double sxs = 1.0 / ((double)l.w / W), sys = 1.0 / ((double)l.h / H);
+        blur_rows_kernel<<<dim3(H, 1, nf), 256, (W + 2 * (l.ksize / 2)) * sizeof(float), st>>>(
+            frames, frame_stride, W, H, hbuf, ncols, same ? 1 : 0, sxs, bt);
+        mark(KIND_BLUR_ROWS, l.k);
         blur_cols_resize_kernel<<<dim3((l.w + 63) / 64, (l.h + 3) / 4, nf), 256, 0, st>>>(
-            hbuf, W, H, img, l.w, l.h, 1.0 / ((double)l.w / W), 1.0 / ((double)l.h / H),
-            same ? 1 : 0, bt);
+            hbuf, ncols, W, H, img, l.w, l.h, sxs, sys, same ? 1 : 0, bt);
+        mark(KIND_BLUR_COLS_RESIZE, l.k);
         poly_exp_kernel<<<dim3((l.w + kPeTileW - 1) / kPeTileW, (l.h + kPeTileH - 1) / kPeTileH,
                                nf),
                           256, 0, st>>>(img, l.w, l.h, R, pt);
+        mark(KIND_POLY_EXP, l.k);
         if (launch_ok("farneback pyramid")) return 1;
 
         float2* fl = l.k == 0 ? (float2*)flows : fbuf[li & 1];
@@ -644,15 +760,29 @@ int farneback_impl(const uint8_t* frames, long frame_stride, int nf, int W, int 
             R, l.w, l.h, fl, M, mode, prev, pw, ph, prev ? 1.0 / ((double)l.w / pw) : 1.0,
             prev ? 1.0 / ((double)l.h / ph) : 1.0, (float)(1.0 / pyr_scale),
             iterations == 0 ? 1 : 0);
-        const size_t lds = (size_t)((kUfTileW + 2 * m) * (kUfTileH + 2 * m) +
-                                    5 * kUfTileH * (kUfTileW + 2 * m)) * sizeof(float);
+        mark(KIND_MATRICES_INIT, l.k);
+        // narrow levels take 128-column strips; rows per workgroup (a multiple
+        // of the LDS batch, 8..32) so that a launch has ~kBfTargetGroups groups
+        const bool narrow = l.w + 2 * m <= 128 || l.w < 400;
+        const int cols = narrow ? 128 : 256;
+        const int strips = (l.w + cols - 2 * m - 1) / (cols - 2 * m);
+        long want = ((long)l.h * strips * pairs + kBfTargetGroups - 1) / kBfTargetGroups;
+        int rows = (int)std::min<long>(32, std::max<long>(kBfBatch, want));
+        rows = (rows + kBfBatch - 1) / kBfBatch * kBfBatch;
+        const dim3 box_grid(strips, (l.h + rows - 1) / rows, pairs);
         for (int it = 0; it < iterations; ++it) {
-            update_flow_kernel<<<dim3((l.w + kUfTileW - 1) / kUfTileW,
-                                      (l.h + kUfTileH - 1) / kUfTileH, pairs),
-                                 256, lds, st>>>(M, l.w, l.h, m, box_scale, fl);
-            if (it < iterations - 1)
+            if (narrow)
+                update_flow_kernel<128><<<box_grid, 128, 0, st>>>(M, l.w, l.h, m, rows, box_scale,
+                                                                   fl);
+            else
+                update_flow_kernel<256><<<box_grid, 256, 0, st>>>(M, l.w, l.h, m, rows, box_scale,
+                                                                   fl);
+            mark(KIND_FLOW, l.k);
+            if (it < iterations - 1) {
                 update_matrices_kernel<<<pix, 256, 0, st>>>(R, l.w, l.h, fl, M, 0, nullptr, 0, 0,
                                                             1.0, 1.0, 1.f, 0);
+                mark(KIND_MATRICES, l.k);
+            }
         }
         if (launch_ok("farneback iterations")) return 1;
         prev = fl;
@@ -698,6 +828,49 @@ int kvp_farneback_flow(const unsigned char* prev, const unsigned char* next, flo
     return kvp::farneback_impl(prev, stride, 2, width, height, pyr_scale, levels, winsize,
                                iterations, poly_n, poly_sigma, flags, workspace, workspace_bytes,
                                flow, stream);
+}
+
+int kvp_farneback_profile(const unsigned char* frames, int num_frames, int width, int height,
+                          double pyr_scale, int levels, int winsize, int iterations, int poly_n,
+                          double poly_sigma, int flags, void* workspace, long workspace_bytes,
+                          float* flows, float* launch_ms, int* launch_kind, int* launch_level,
+                          int capacity, int* count, void* stream) {
+    if (!launch_ms || !launch_kind || !launch_level || !count) {
+        kvp::set_error("farneback_profile: null output array");
+        return 1;
+    }
+    kvp::Timeline tl;
+    tl.st = (hipStream_t)stream;
+    const int rc = kvp::farneback_impl(frames, (long)width * height, num_frames, width, height,
+                                       pyr_scale, levels, winsize, iterations, poly_n,
+                                       poly_sigma, flags, workspace, workspace_bytes, flows,
+                                       stream, &tl);
+    if (rc) return rc;
+    if (!tl.ok || tl.ev.empty()) {
+        kvp::set_error("farneback_profile: event creation failed");
+        return 1;
+    }
+    if (hipEventSynchronize(tl.ev.back()) != hipSuccess) {
+        kvp::set_error("farneback_profile: event synchronize failed");
+        return 1;
+    }
+    const int n = (int)tl.ev.size() - 1;
+    *count = n;
+    if (n > capacity) {
+        kvp::set_error("farneback_profile: %d launches > capacity %d", n, capacity);
+        return 1;
+    }
+    for (int i = 0; i < n; ++i) {
+        float ms = 0.f;
+        if (hipEventElapsedTime(&ms, tl.ev[i], tl.ev[i + 1]) != hipSuccess) {
+            kvp::set_error("farneback_profile: elapsed time unavailable");
+            return 1;
+        }
+        launch_ms[i] = ms;
+        launch_kind[i] = tl.kind[i + 1];
+        launch_level[i] = tl.level[i + 1];
+    }
+    return 0;
 }
 
 int kvp_motion_change_rates(const float* flows, int pairs, int width, int height, int grid_rows,

@@ -151,6 +151,9 @@ SIGNATURES = {
     "kvp_farneback_flow": (c_int, [c_void_p, c_void_p, c_void_p, c_int, c_int, c_double, c_int,
                                    c_int, c_int, c_int, c_double, c_int, c_void_p, c_long,
                                    c_void_p]),
+    "kvp_farneback_profile": (c_int, [c_void_p, c_int, c_int, c_int, c_double, c_int, c_int,
+                                      c_int, c_int, c_double, c_int, c_void_p, c_long, c_void_p,
+                                      c_void_p, c_void_p, c_void_p, c_int, c_void_p, c_void_p]),
     "kvp_motion_change_rates": (c_int, [c_void_p, c_int, c_int, c_int, c_int, c_int, c_int,
                                         c_void_p, c_void_p, c_void_p]),
 }

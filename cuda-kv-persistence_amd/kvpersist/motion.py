@@ -99,6 +99,38 @@ def farneback_flows(frames, flows: torch.Tensor | None = None, stream: int | Non
     return flows
 
 
+KINDS = ("blur_rows", "blur_cols_resize", "poly_exp", "matrices_init", "box_flow", "matrices")
+
+
+def farneback_profile(frames, flows: torch.Tensor | None = None, stream: int | None = None,
+                      **params):
+    """farneback_flows with an event after every launch (synchronises):
+    -> (flows, [(kind name, pyramid level, ms), ...] in launch order)."""
+    fr = _frames_u8(frames)
+    n, H, W = fr.shape
+    p = _params(params)
+    lib = _lib.load()
+    need = lib.kvp_farneback_workspace_bytes(n, W, H, float(p["pyr_scale"]), int(p["levels"]))
+    if need < 0:
+        raise ValueError(f"bad clip shape {tuple(fr.shape)} or pyramid parameters {p}")
+    ws = _workspace(fr.device, need)
+    if flows is None:
+        flows = torch.empty(n - 1, H, W, 2, dtype=torch.float32, device=fr.device)
+    cap = 1024
+    ms = np.zeros(cap, dtype=np.float32)
+    kind = np.zeros(cap, dtype=np.int32)
+    level = np.zeros(cap, dtype=np.int32)
+    count = np.zeros(1, dtype=np.int32)
+    _check(lib.kvp_farneback_profile(_ptr(fr), n, W, H, float(p["pyr_scale"]), int(p["levels"]),
+                                     int(p["winsize"]), int(p["iterations"]), int(p["poly_n"]),
+                                     float(p["poly_sigma"]), int(p["flags"]), _ptr(ws),
+                                     ws.numel(), _ptr(flows), ms.ctypes.data, kind.ctypes.data,
+                                     level.ctypes.data, cap, count.ctypes.data, stream),
+           "kvp_farneback_profile")
+    k = int(count[0])
+    return flows, [(KINDS[kind[i]], int(level[i]), float(ms[i])) for i in range(k)]
+
+
 def calc_optical_flow_farneback(prev, next, flow=None, pyr_scale=0.5, levels=3, winsize=15,
                                 iterations=3, poly_n=5, poly_sigma=1.2, flags=0,
                                 stream: int | None = None) -> torch.Tensor:

@@ -165,3 +165,29 @@ def qkv_device(frames: int, tokens: int, *, seed: int, dtype, device="cuda",
         x = torch.randn(shape, generator=g, device=device, dtype=torch.float32)
         out.append(x.to(dtype))
     return tuple(out)
+
+
+def synthetic_clip(frames: int, height: int = 480, width: int = 832, *, seed: int = 0,
+                   max_shift: float = 2.0):
+    """uint8 gray clip [frames, height, width] for the motion producer: a smooth
+    random texture (Gaussian-filtered noise, sigma 2 px) whose content moves
+    by a random-walk global shift (up to max_shift px per frame and axis)
+    plus a drifting sinusoidal local warp of 1.5 px. Synthetic input only
+    (the reference reads a DAVIS / mp4 clip through OpenCV)."""
+    from scipy.ndimage import map_coordinates
+    rng = np.random.default_rng(seed)
+    pad = 48
+    base = gaussian_filter(rng.standard_normal((height + 2 * pad, width + 2 * pad)), 2.0,
+                           mode="wrap")
+    base = (base - base.mean()) / (base.std() + 1e-12)
+    yy, xx = np.mgrid[0:height, 0:width].astype(np.float64)
+    out = np.empty((frames, height, width), dtype=np.uint8)
+    ox = oy = 0.0
+    for f in range(frames):
+        warp = 1.5 * np.sin(2 * math.pi * (xx / width + 0.05 * f)) * np.cos(
+            2 * math.pi * yy / height)
+        img = map_coordinates(base, [yy + pad + oy, xx + pad + ox + warp], order=1, mode="wrap")
+        out[f] = np.clip(np.rint(128 + 40 * img), 0, 255).astype(np.uint8)
+        ox += rng.uniform(-max_shift, max_shift)
+        oy += rng.uniform(-max_shift, max_shift)
+    return out

@@ -56,6 +56,21 @@ int kvp_farneback_flow(const unsigned char* prev, const unsigned char* next,
                        double poly_sigma, int flags, void* workspace,
                        long workspace_bytes, void* stream);
 
+/* kvp_farneback_flows with an event after every kernel launch, for
+ * measurement (no counterpart in the reference, whose flow is a cv2 call):
+ * launch i took launch_ms[i] on `stream`; launch_kind[i] is 0 pre-blur rows,
+ * 1 pre-blur columns + resize, 2 polynomial expansion, 3 first matrix update
+ * of a level (initial flow), 4 box filter + flow solve, 5 matrix update;
+ * launch_level[i] is the pyramid level (0 = full size). Synchronises the
+ * stream. *count receives the number of launches (an error if > capacity). */
+int kvp_farneback_profile(const unsigned char* frames, int num_frames,
+                          int width, int height, double pyr_scale, int levels,
+                          int winsize, int iterations, int poly_n,
+                          double poly_sigma, int flags, void* workspace,
+                          long workspace_bytes, float* flows, float* launch_ms,
+                          int* launch_kind, int* launch_level, int capacity,
+                          int* count, void* stream);
+
 /* Per-pair change rates (reference: gen_motion_from_video.py:61-67,112-121):
  * mag = |flow|; cell_maps fp32 [pairs, grid_rows, grid_cols] = mean of mag
  * over (height/grid_rows) x (width/grid_cols) pixel cells; change fp64

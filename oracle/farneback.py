@@ -73,8 +73,6 @@ rule) follow its published source, and no vector from cv2 checks them.
 
 from __future__ import annotations
 
-import math
-
 import numpy as np
 
 MIN_SIZE = 32
@@ -392,26 +390,4 @@ def trace_rows(change: np.ndarray, tau: float, reuse: np.ndarray, tokens: int,
             cnt = tile_tokens if t < tiles - 1 else tokens - (tiles - 1) * tile_tokens
             out.append([f, t, f"{change[f, t]:.6f}", int(change[f, t] < tau), t * tile_tokens,
                         int(cnt), int(reuse[f, t])])
-    return out
-
-
-def synthetic_clip(frames: int, height: int, width: int, *, seed: int = 0,
-                   max_shift: float = 2.0) -> np.ndarray:
-    """uint8 [frames, H, W]: a smooth random texture whose content moves by a
-    per-frame global shift plus a slowly drifting local warp. Test input only."""
-    rng = np.random.default_rng(seed)
-    pad = 48
-    base = rng.standard_normal((height + 2 * pad, width + 2 * pad))
-    from scipy.ndimage import gaussian_filter, map_coordinates
-    base = gaussian_filter(base, 2.0, mode="wrap")
-    base = (base - base.mean()) / (base.std() + 1e-12)
-    yy, xx = np.mgrid[0:height, 0:width].astype(np.float64)
-    out = np.empty((frames, height, width), dtype=np.uint8)
-    ox = oy = 0.0
-    for f in range(frames):
-        warp = 1.5 * np.sin(2 * math.pi * (xx / width + 0.05 * f)) * np.cos(2 * math.pi * yy / height)
-        img = map_coordinates(base, [yy + pad + oy, xx + pad + ox + warp], order=3, mode="wrap")
-        out[f] = np.clip(np.rint(128 + 40 * img), 0, 255).astype(np.uint8)
-        ox += rng.uniform(-max_shift, max_shift)
-        oy += rng.uniform(-max_shift, max_shift)
     return out

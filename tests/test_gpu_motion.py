@@ -21,6 +21,7 @@ import torch
 from scipy import ndimage
 
 from kvpersist import motion
+from kvpersist import workloads
 from oracle import farneback as fb
 
 pytestmark = pytest.mark.gpu
@@ -50,7 +51,7 @@ def _flow_ok(got, want, what=""):
 
 @pytest.mark.parametrize("H,W,frames", [(96, 128, 3), (256, 320, 3), (480, 832, 3)])
 def test_clip_flows_match_oracle(H, W, frames):
-    clip = fb.synthetic_clip(frames, H, W, seed=H + W)
+    clip = workloads.synthetic_clip(frames, H, W, seed=H + W)
     got = motion.farneback_flows(clip).cpu().numpy()
     want = fb.farneback_clip(clip)
     assert got.shape == want.shape == (frames - 1, H, W, 2)
@@ -61,14 +62,14 @@ def test_clip_flows_match_oracle(H, W, frames):
                                     dict(poly_n=7, poly_sigma=1.5, pyr_scale=0.6, levels=2),
                                     dict(iterations=0), dict(winsize=14)])
 def test_parameter_variants_match_oracle(params):
-    clip = fb.synthetic_clip(2, 128, 160, seed=7)
+    clip = workloads.synthetic_clip(2, 128, 160, seed=7)
     got = motion.calc_optical_flow_farneback(clip[0], clip[1], **params).cpu().numpy()
     want = fb.calc_optical_flow_farneback(clip[0], clip[1], **params)
     _flow_ok(got, want, str(params))
 
 
 def test_pair_entry_equals_clip_entry_bitwise():
-    clip = fb.synthetic_clip(4, 480, 832, seed=1)
+    clip = workloads.synthetic_clip(4, 480, 832, seed=1)
     flows = motion.farneback_flows(clip)
     dev = torch.from_numpy(clip).to(DEV)
     for p in range(3):
@@ -119,7 +120,7 @@ def test_change_rates_match_oracle():
 
 
 def test_motion_trace_matches_oracle_post_processing(tmp_path):
-    clip = fb.synthetic_clip(5, 480, 832, seed=9)
+    clip = workloads.synthetic_clip(5, 480, 832, seed=9)
     tr = motion.motion_trace(clip)
     flows = motion.farneback_flows(clip).cpu().numpy()
     _, pairs = fb.change_rates(flows, 30, 52, 16)
@@ -140,7 +141,7 @@ def test_motion_trace_matches_oracle_post_processing(tmp_path):
 
 
 def test_bad_arguments_raise():
-    clip = fb.synthetic_clip(2, 64, 64, seed=2)
+    clip = workloads.synthetic_clip(2, 64, 64, seed=2)
     with pytest.raises(RuntimeError, match="flags"):
         motion.calc_optical_flow_farneback(clip[0], clip[1], flags=256)
     with pytest.raises(RuntimeError, match="winsize"):

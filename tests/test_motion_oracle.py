@@ -12,6 +12,7 @@ import numpy as np
 import pytest
 from scipy import ndimage
 
+from kvpersist import workloads
 from oracle import farneback as fb
 
 
@@ -169,7 +170,7 @@ def test_subpixel_translation_is_recovered(dx, dy):
 
 
 def test_clip_pairs_equal_single_pairs():
-    clip = fb.synthetic_clip(3, 64, 96, seed=3)
+    clip = workloads.synthetic_clip(3, 64, 96, seed=3)
     flows = fb.farneback_clip(clip)
     for p in range(2):
         assert np.array_equal(flows[p], fb.calc_optical_flow_farneback(clip[p], clip[p + 1]))
