@@ -327,6 +327,16 @@ def motion_bench(args, torch, stream):
                 "per_launch": f"{MOTION_BYTES_PER_PX[kind]} B/px x {P} px x {units} "
                               f"{'frames' if kind in MOTION_PER_FRAME else 'pairs'}"}
 
+    # fabric bytes of the level-0 launches from rocprofv3 FETCH_SIZE / WRITE_SIZE
+    # runs of this workload, scaled by a copy-kernel calibration (committed)
+    traffic = None
+    tfile = ROOT / "profiles" / "motion_farneback_traffic.json"
+    if tfile.exists():
+        try:
+            rec = json.loads(tfile.read_text())["kernels"].get(dominant)
+            traffic = rec["hbm_bytes_per_launch"] if rec else None
+        except (OSError, ValueError, KeyError):
+            traffic = None
     out = {
         "metric": "motion producer ms per frame pair (Farneback flow + tile change rates)",
         "value": round(clip_ms / pairs, 5),
@@ -341,7 +351,7 @@ def motion_bench(args, torch, stream):
                    "frames": n, "dtype": "f32"},
         "launch_ms_per_clip": {k: round(v, 4) for k, v in per_kind.items()},
         "launches_per_clip": len(launches),
-        "roofline": dict(level0_roof(dominant), kernel=dominant),
+        "roofline": dict(level0_roof(dominant), kernel=dominant, traffic=traffic),
         "level0_rooflines": {k: level0_roof(k) for k in lvl0},
     }
     if not args.no_cpu_baseline:
