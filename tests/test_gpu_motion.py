@@ -140,6 +140,41 @@ def test_motion_trace_matches_oracle_post_processing(tmp_path):
     assert meta["farneback"] == motion.FARNEBACK
 
 
+def test_trace_drives_the_policy_cli(tmp_path):
+    """The written trace feeds policy_experiment --motion-csv (reference
+    CSV columns incl. reuse): reuse_weighted in streaming mode runs on it and
+    leaves the attention output bit-identical to policy none."""
+    import subprocess
+    from kvpersist import _lib
+    frames, tokens, hidden, heads, tt = 3, 1560, 256, 2, 16
+    tr = motion.motion_trace(workloads.synthetic_clip(frames, 480, 832, seed=4))
+    csv_path, _ = motion.write_trace(tr, tmp_path)
+    rng = np.random.default_rng(8)
+    paths = []
+    for name in "qkv":
+        p = tmp_path / f"{name}.bin"
+        rng.standard_normal((frames * tokens, hidden), dtype=np.float32).tofile(p)
+        paths.append(p)
+    common = ["--attn-mode", "cross", "--q", str(paths[0]), "--k", str(paths[1]), "--v",
+              str(paths[2]), "--frames", str(frames), "--tokens", str(tokens), "--hidden",
+              str(hidden), "--heads", str(heads), "--tile-tokens", str(tt)]
+
+    def run(args):
+        return subprocess.run([str(_lib.CLI_PATH), *args], capture_output=True, text=True,
+                              timeout=120)
+    r0 = run(["--policy", "none", "--out", str(tmp_path / "none.bin"), *common])
+    assert r0.returncode == 0, r0.stderr
+    r1 = run(["--policy", "reuse_weighted", "--streaming", "--motion-csv", str(csv_path),
+              "--out", str(tmp_path / "rw.bin"), "--set-aside-bytes", str(8 * tt * hidden * 8),
+              *common])
+    assert r1.returncode == 0, r1.stderr
+    assert r1.stdout.splitlines()[0].startswith("policy=reuse_weighted slots=8")
+    assert any(ln.startswith("streamed staged_bytes=") for ln in r1.stdout.splitlines())
+    a = np.fromfile(tmp_path / "none.bin", dtype=np.float32)
+    b = np.fromfile(tmp_path / "rw.bin", dtype=np.float32)
+    assert a.size == frames * tokens * hidden and np.array_equal(a, b)
+
+
 def test_bad_arguments_raise():
     clip = workloads.synthetic_clip(2, 64, 64, seed=2)
     with pytest.raises(RuntimeError, match="flags"):
