@@ -68,6 +68,30 @@ def test_parameter_variants_match_oracle(params):
     _flow_ok(got, want, str(params))
 
 
+@pytest.mark.parametrize("H,W", [(77, 101), (12, 10), (70, 130)])
+def test_odd_and_minimum_sizes_match_oracle(H, W):
+    """Widths that are not a multiple of 4 (byte loads), the 10-pixel minimum
+    side, and coarser levels whose sides round half to even (77 x 101 ->
+    38 x 50, 70 x 130 -> 35 x 65)."""
+    clip = workloads.synthetic_clip(3, H, W, seed=W)
+    got = motion.farneback_flows(clip).cpu().numpy()
+    _flow_ok(got, fb.farneback_clip(clip), f"{H}x{W}")
+
+
+def test_unaligned_pair_pointers_equal_aligned():
+    """Frames at odd byte offsets of one allocation (the pair entry takes any
+    two pointers) give the same flow as the aligned clip entry."""
+    clip = workloads.synthetic_clip(2, 96, 128, seed=11)
+    flat = torch.zeros(2 * 96 * 128 + 8, dtype=torch.uint8, device=DEV)
+    a = flat[1:1 + 96 * 128].view(96, 128)
+    b = flat[3 + 96 * 128:3 + 2 * 96 * 128].view(96, 128)
+    a.copy_(torch.from_numpy(clip[0]))
+    b.copy_(torch.from_numpy(clip[1]))
+    got = motion.calc_optical_flow_farneback(a, b)
+    want = motion.farneback_flows(clip)[0]
+    assert torch.equal(got, want)
+
+
 def test_pair_entry_equals_clip_entry_bitwise():
     clip = workloads.synthetic_clip(4, 480, 832, seed=1)
     flows = motion.farneback_flows(clip)
