@@ -199,6 +199,30 @@ def test_trace_drives_the_policy_cli(tmp_path):
     assert a.size == frames * tokens * hidden and np.array_equal(a, b)
 
 
+def test_command_line_writes_the_trace(tmp_path):
+    """python -m kvpersist.motion --frames-npy clip.npy (the script's outputs:
+    CSV rows and meta JSON, grid and tile size from a grounding config)."""
+    import json
+    import subprocess
+    import sys
+    clip = workloads.synthetic_clip(4, 480, 832, seed=12)
+    np.save(tmp_path / "clip.npy", clip)
+    cfg = tmp_path / "grounding.json"
+    cfg.write_text(json.dumps({"model": {"latent_grid": [30, 52], "tile_size_tokens": 16}}))
+    out = tmp_path / "traces"
+    r = subprocess.run([sys.executable, "-m", "kvpersist.motion", "--frames-npy",
+                        str(tmp_path / "clip.npy"), "--out-dir", str(out), "--config", str(cfg),
+                        "--frames", "3"], capture_output=True, text=True, timeout=240,
+                       cwd=str(motion.Path(motion.__file__).resolve().parents[1]))
+    assert r.returncode == 0, r.stderr
+    assert "tiles/frame: 98  rows written: 294" in r.stdout
+    rows = (out / "motion_trace_real.csv").read_text().splitlines()
+    assert len(rows) == 1 + 3 * 98
+    meta = json.loads((out / "trace_real_meta.json").read_text())
+    assert meta["frames"] == 3 and meta["size"] == [832, 480]
+    assert 0.0 <= meta["reuse_fraction_achieved"] <= 1.0
+
+
 def test_bad_arguments_raise():
     clip = workloads.synthetic_clip(2, 64, 64, seed=2)
     with pytest.raises(RuntimeError, match="flags"):
