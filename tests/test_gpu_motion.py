@@ -223,6 +223,45 @@ def test_command_line_writes_the_trace(tmp_path):
     assert 0.0 <= meta["reuse_fraction_achieved"] <= 1.0
 
 
+def test_full_flow_clip_and_latents_to_gated_attention():
+    """The reference's whole flow on the device: a clip's Farneback change
+    rates (the motion producer) rank the tiles, a bf16 backbone produces
+    layer K/V from latents (the K/V producer), and the motion-gated
+    cross-frame pipeline stages the top-ranked tiles into the arena. The
+    output equals policy none bit for bit, the arena holds tiles, and the
+    attention is within the bf16 bar of the oracle."""
+    from kvpersist import FramePipeline
+    from kvpersist import backbone as kb
+    from oracle import attention as at
+    frames, T, heads = 3, 1560, 12
+    D = heads * 128
+    tr = motion.motion_trace(workloads.synthetic_clip(frames, 480, 832, seed=13))
+    scores = tr.change.astype(np.float32)                     # [frames, 98]
+    cfg = kb.BackboneConfig(num_layers=2, hidden_dim=D, num_heads=heads)
+    model = kb.SelfAttentionBackbone(cfg, seed=31, dtype="bf16")
+    lat = torch.randn(frames, 16, 30, 52, generator=torch.Generator(device=DEV).manual_seed(3),
+                      device=DEV)
+    _, k, v, q = model.forward_token_major(lat, keep_q=True)
+    ql, kl, vl = q[1].contiguous(), k[1].contiguous(), v[1].contiguous()
+    outs = {}
+    for policy, aside in (("none", 0), ("motion", 64 * 16 * 2 * D * 2)):
+        pl = FramePipeline(policy, cross=True, streaming=False, frames=frames, T=T, D=D,
+                           heads=heads, tile_tokens=16, set_aside_bytes=aside, dtype=1)
+        pl.set_scores(scores.reshape(-1))
+        out = torch.empty_like(ql)
+        pl.run(ql, kl, vl, out)
+        torch.cuda.synchronize()
+        if policy == "motion":
+            assert pl.staged_tiles() > 0
+        outs[policy] = out.cpu()
+        pl.close()
+    assert torch.equal(outs["none"], outs["motion"])
+    want = at.attention_frames(ql.float().cpu(), kl.float().cpu(), vl.float().cpu(), frames, T,
+                               heads, "cross")
+    assert float((outs["none"].float() - want).abs().max()) <= 2e-2
+    model.close()
+
+
 def test_bad_arguments_raise():
     clip = workloads.synthetic_clip(2, 64, 64, seed=2)
     with pytest.raises(RuntimeError, match="flags"):
