@@ -262,6 +262,51 @@ def test_full_flow_clip_and_latents_to_gated_attention():
     model.close()
 
 
+def test_file_flow_backbone_bins_and_trace_drive_the_cli(tmp_path):
+    """The reference's file-based flow: the motion trace CSV of a clip
+    (gen_motion_from_video), one backbone layer's q/k/v exported as flat fp32
+    bins (export_bins), then policy_experiment over both — motion-gated
+    output bit-identical to policy none and within the fp32 bar of the
+    oracle."""
+    import subprocess
+    from kvpersist import _lib, export_bins
+    from kvpersist import backbone as kb
+    from oracle import attention as at
+    frames, T, heads = 3, 1560, 2
+    D = heads * 128
+    tr = motion.motion_trace(workloads.synthetic_clip(frames, 480, 832, seed=14))
+    csv_path, _ = motion.write_trace(tr, tmp_path)
+    model = kb.SelfAttentionBackbone(kb.BackboneConfig(num_layers=1, hidden_dim=D,
+                                                       num_heads=heads), seed=5, dtype="fp32")
+    lat = torch.randn(frames, 16, 30, 52, generator=torch.Generator(device=DEV).manual_seed(6),
+                      device=DEV)
+    _, k, v, q = model.forward_token_major(lat, keep_q=True)
+    qp, kp, vp = export_bins.export_layer(q[0], k[0], v[0], tmp_path, "L0")
+    model.close()
+    common = ["--attn-mode", "cross", "--q", str(qp), "--k", str(kp), "--v", str(vp),
+              "--frames", str(frames), "--tokens", str(T), "--hidden", str(D), "--heads",
+              str(heads), "--tile-tokens", "16"]
+
+    def run(args):
+        return subprocess.run([str(_lib.CLI_PATH), *args], capture_output=True, text=True,
+                              timeout=120)
+    r0 = run(["--policy", "none", "--out", str(tmp_path / "none.bin"), *common])
+    assert r0.returncode == 0, r0.stderr
+    r1 = run(["--policy", "motion", "--motion-csv", str(csv_path), "--out",
+              str(tmp_path / "m.bin"), "--set-aside-bytes", str(22 * 16 * D * 8), *common])
+    assert r1.returncode == 0, r1.stderr
+    assert r1.stdout.splitlines()[0].startswith("policy=motion slots=22")
+    a = np.fromfile(tmp_path / "none.bin", dtype=np.float32).reshape(frames * T, D)
+    b = np.fromfile(tmp_path / "m.bin", dtype=np.float32).reshape(frames * T, D)
+    assert np.array_equal(a, b)
+    qh = torch.from_numpy(np.fromfile(qp, dtype=np.float32).reshape(frames * T, D))
+    kh = torch.from_numpy(np.fromfile(kp, dtype=np.float32).reshape(frames * T, D))
+    vh = torch.from_numpy(np.fromfile(vp, dtype=np.float32).reshape(frames * T, D))
+    want = at.attention_frames(qh, kh, vh, frames, T, heads, "cross").numpy()
+    err = np.abs(a - want)
+    assert err.max() <= 1e-3 and err.mean() <= 1e-4, (err.max(), err.mean())
+
+
 def test_bad_arguments_raise():
     clip = workloads.synthetic_clip(2, 64, 64, seed=2)
     with pytest.raises(RuntimeError, match="flags"):
