@@ -231,6 +231,25 @@ def trace_rows(trace: MotionTrace):
     return rows
 
 
+def read_trace_csv(path) -> np.ndarray:
+    """motion_score column of a trace CSV -> float32 [frames, tiles], parsed
+    as the reference's driver does (%f into a float; reference:
+    src/run_policy_experiment.cu:45-69)."""
+    rows = []
+    with open(path, newline="") as fh:
+        r = csv.reader(fh)
+        next(r)                                    # header
+        for rec in r:
+            if rec:
+                rows.append((int(rec[0]), int(rec[1]), np.float32(rec[2])))
+    frames = max(f for f, _, _ in rows) + 1
+    tiles = max(t for _, t, _ in rows) + 1
+    out = np.zeros((frames, tiles), dtype=np.float32)
+    for f, t, v in rows:
+        out[f, t] = v
+    return out
+
+
 def trace_meta(trace: MotionTrace, source: str = "") -> dict:
     """The reference's provenance and validation block (gen_motion_from_video.py:154-176)."""
     grid = trace.cell_maps.shape[1:]

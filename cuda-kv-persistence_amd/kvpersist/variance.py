@@ -32,6 +32,7 @@ cannot pin MI355X clocks, and fabric bytes do not depend on the clock.
 Usage on the GPU box, from the repository root:
 
     python3 -m kvpersist.variance [--smoke] [--out profiles/variance_c4.md]
+                                  [--motion-csv motion_trace_real.csv]
 
 The analysis functions (`window_bytes`, `abba_orders`, `combo_stats`,
 `policy_deltas`, `separated`) are plain Python for tests.
@@ -123,6 +124,9 @@ def policy_deltas(stats, mode):
     return out
 
 
+TRACE_ENV = "KVP_VARIANCE_MOTION_CSV"   # passes --motion-csv to the profiled children
+
+
 def separated(stats, mode, a="reuse_weighted", b="recency"):
     return not overlap(stats[(mode, a)], stats[(mode, b)])
 
@@ -143,7 +147,15 @@ def child(mode, policy, out_json):
                        heads=H, tile_tokens=workloads.TILE_TOKENS,
                        set_aside_bytes=cfg.set_aside,
                        dtype=BF16, window_frames=cfg.window)
-    pl.set_scores(workloads.motion_for(cfg, 0))
+    trace = os.environ.get(TRACE_ENV)
+    if trace:
+        from kvpersist.motion import read_trace_csv
+        scores = read_trace_csv(trace)
+        if scores.shape != (F, cfg.num_tiles):
+            raise ValueError(f"{trace}: scores {scores.shape}, C4 needs ({F}, {cfg.num_tiles})")
+    else:
+        scores = workloads.motion_for(cfg, 0)
+    pl.set_scores(scores)
     pl.run(q, k, v, out)
     torch.cuda.synchronize()
     digest = hashlib.sha256(out.view(torch.int16).cpu().numpy().tobytes()).hexdigest()
@@ -194,7 +206,13 @@ def main(argv=None):
     ap.add_argument("--smoke", action="store_true", help="one combo, one repeat")
     ap.add_argument("--out", default=str(ROOT / "profiles" / "variance_c4.md"))
     ap.add_argument("--timeout", type=int, default=180, help="seconds per profiled run")
+    ap.add_argument("--motion-csv", default=None,
+                    help="motion trace CSV (frame_id,tile_id,motion_score,...; 50 x 98 rows) "
+                         "instead of the synthetic C4 scores, as the reference runs its "
+                         "real-motion trace")
     args = ap.parse_args(argv)
+    if args.motion_csv:
+        os.environ[TRACE_ENV] = str(Path(args.motion_csv).resolve())
     if args.child:
         child(*args.child)
         return 0
@@ -232,6 +250,9 @@ def main(argv=None):
           "`rocprofv3 --pmc` passes (`FETCH_SIZE`; `TCC_HIT_sum TCC_MISS_sum`) restricted to "
           f"`{KERNEL}`; window = attention launches {SKIP}..{SKIP + COUNT - 1} of 50; "
           f"{repeats} repeat(s), ABBA order; reads scaled x{factor:g} (copy calibration).\n",
+          "Motion scores: " + (f"`{Path(args.motion_csv).name}` (`--motion-csv`)"
+                               if args.motion_csv else
+                               "the synthetic C4 field (`workloads.motion_for`)") + ".\n",
           f"Bitwise gate (every policy's output equals none's, same mode and repeat): "
           f"{'PASS' if gate else 'FAIL'}\n",
           "| mode | policy | window reads median | min | max | spread | L2 hit median | verdict |",
