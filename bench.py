@@ -61,6 +61,9 @@ def parse():
     ap.add_argument("--profile-policy", default=None,
                     help="run exactly one 30-layer step of this policy's pipeline and exit "
                          "(for rocprofv3 --pmc byte counting per policy)")
+    ap.add_argument("--set-aside-tiles", type=int, default=None,
+                    help="arena size in 16-token bf16 tiles (default: the configuration's "
+                         "22); with --profile-policy, for the arena residency study")
     ap.add_argument("--no-producer", action="store_true",
                     help="skip the upstream K/V producer measurement")
     ap.add_argument("--producer-only", action="store_true",
@@ -423,9 +426,13 @@ def main():
     torch.cuda.synchronize()
     log("inputs resident")
 
+    # one arena tile = 16 token rows of [K row | V row] in bf16
+    set_aside = (cfg.set_aside if args.set_aside_tiles is None
+                 else args.set_aside_tiles * 16 * 2 * D * 2)
+
     def make(policy):
         return FramePipeline(policy, cross=True, streaming=args.streaming, frames=F, T=T, D=D,
-                             heads=H, tile_tokens=16, set_aside_bytes=cfg.set_aside,
+                             heads=H, tile_tokens=16, set_aside_bytes=set_aside,
                              dtype=api.BF16)
 
     def run_step(pl):
@@ -446,13 +453,20 @@ def main():
         return e0.elapsed_time(e1) / steps, wall / steps
 
     if args.profile_policy:
+        # one step (what the rocprofv3 passes count); --steps > 1 also times
+        # steps 2.. with HIP events (meaningful only outside the profiler)
         pl = make(args.profile_policy)
         torch.cuda.synchronize()
         run_step(pl)
         torch.cuda.synchronize()
+        rec = {"profile_policy": args.profile_policy, "set_aside_bytes": set_aside,
+               "staged_tiles_last_frame": pl.staged_tiles(), "layers": layers, "frames": F,
+               "query_frames": layers * F}
+        if args.steps > 1:
+            ms, _ = timed(pl, args.steps - 1)
+            rec["ms_per_frame"] = round(ms / F, 4)
         pl.close()
-        print(json.dumps({"profile_policy": args.profile_policy, "layers": layers,
-                          "frames": F, "query_frames": layers * F}), flush=True)
+        print(json.dumps(rec), flush=True)
         return
 
     # --- headline: policy pipeline, K timed steps -----------------------------------
