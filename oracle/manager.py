@@ -22,7 +22,12 @@ scenario S1-S8 with its published numbers (reference:
 tests/test_capacity_admission.py:80-148, configs/grounding_config.json:29-50)
 and hand-derived slot sequences for the arena and streaming rules (LIFO
 reuse, sticky hits, refusals leaving state unchanged, the intra-streaming
-release quirk of src/run_policy_experiment.cu:180-185).
+release quirk of src/run_policy_experiment.cu:180-185). The cross-frame
+plan (tests/test_plan_pins.py): per-frame KVMap prefixes and copy lists
+worked out by hand for recency and motion, arena and streaming, a sliding
+window and a short last tile, each with planted mistakes (source row
+without its frame term, release after staging, release in descending id
+order) that must fail.
 """
 
 from __future__ import annotations
@@ -152,10 +157,20 @@ class ManagerModel:
         self.high_water = -1
 
 
+PLANTS = ("drop_src_frame", "release_after_stage", "release_descending")
+
+
 def plan_frames(policy: str, *, cross: bool, streaming: bool, frames: int, T: int, D: int,
                 tile_tokens: int, set_aside: int, elem: int, scores_flat,
-                window_frames: int = 0) -> list[dict]:
-    """Per-frame driver plan; elem = bytes per element (4 fp32, 2 bf16)."""
+                window_frames: int = 0, _plant: str | None = None) -> list[dict]:
+    """Per-frame driver plan; elem = bytes per element (4 fp32, 2 bf16).
+
+    `_plant` plants one deliberate mistake for the pin tests (one of PLANTS):
+    the source row without its frame term (tile rows of frame 0 instead of
+    frame src_f), the streaming release after the frame's staging instead of
+    before it, or the release walking dropped tiles in descending id order.
+    """
+    assert _plant is None or _plant in PLANTS
     num_tiles = (T + tile_tokens - 1) // tile_tokens
     persist = policy != "none"
     out = []
@@ -191,8 +206,11 @@ def plan_frames(policy: str, *, cross: bool, streaming: bool, frames: int, T: in
         for i in ids:
             if 0 <= i < selected.size:
                 selected[i] = True
-        if streaming and f > 0:
-            for gid in range(prev_selected.size):
+        def release_dropped():
+            order = range(prev_selected.size)
+            if _plant == "release_descending":
+                order = reversed(order)
+            for gid in order:
                 if not prev_selected[gid]:
                     continue
                 if gid < selected.size and selected[gid]:
@@ -203,6 +221,9 @@ def plan_frames(policy: str, *, cross: bool, streaming: bool, frames: int, T: in
                 c = min(tile_tokens, T - t0)
                 for r in range(c):
                     mgr.streaming_release(src_f * T + t0 + r)
+
+        if streaming and f > 0 and _plant != "release_after_stage":
+            release_dropped()
         mgr.arena_begin_step()
         h_map[:(f + 1) * T] = -1
         copies = []
@@ -215,7 +236,7 @@ def plan_frames(policy: str, *, cross: bool, streaming: bool, frames: int, T: in
             ok = True
             r = 0
             while r < c and ok:
-                row_id = src_f * T + t0 + r
+                row_id = (0 if _plant == "drop_src_frame" else src_f * T) + t0 + r
                 if streaming:
                     ok, slot, restaged = mgr.streaming_stage(row_id, row_bytes, row_bytes)
                     if ok:
@@ -231,6 +252,8 @@ def plan_frames(policy: str, *, cross: bool, streaming: bool, frames: int, T: in
                 r += 1
             if ok:
                 staged_tiles += 1
+        if streaming and f > 0 and _plant == "release_after_stage":
+            release_dropped()
         if streaming:
             prev_selected = selected
         else:
