@@ -43,7 +43,6 @@
 
 #include "kvp_c_api.h"
 #include "kvp_internal.h"
-#include "stage_runs.h"
 
 namespace kvp {
 namespace {
@@ -73,13 +72,21 @@ struct AttnArgs {
     const long* kvmap;
     void* out;
     void* part_o;     // [splits][frames][nq][D] normalised partial O:
-                      // fp16 from the bf16 kernel, fp32 from the fp32 kernel
+                      // fp16 from the bf16 kernel (row scaled by 2^e),
+                      // fp32 from the fp32 kernel
     float* part_lse;  // [splits][frames][heads][nq] log2-sum-exp
+    float* part_exp;  // [splits][frames][heads][nq] e of the fp16 row scale
     long q_fstride;   // elements between frames of q / out
     long kv_fstride;  // elements between frames of k / v
     long map_fstride; // entries between frames of kvmap
+    long arena_fstride; // bytes between per-frame arena regions (0: one arena)
+    // Key range of frame i of the launch: [max(key_begin, e - max_span), e)
+    // with e = key_end + i * kend_step (kend_step = T for a causal layer
+    // launch, 0 when every frame attends the same range).
     long key_begin;
     long key_end;
+    long kend_step;
+    long max_span;
     long keys_per_split;
     int nq;
     int D;
@@ -87,6 +94,7 @@ struct AttnArgs {
     int frames;
     int splits;
     int nqb;
+    int layer_order;   // 1: XCD-column work order, frames longest first
     float scale_log2;  // log2(e) / sqrt(head_dim)
 };
 
@@ -101,11 +109,41 @@ __device__ __forceinline__ int xcd_remap(int bid, int n) {
 
 struct WgCoord {
     int qb, split, head, frame;
+    bool valid;
 };
 
+// Number of (head, q-block) columns XCD x owns in the layer work order.
+__host__ __device__ __forceinline__ int xcd_columns(int cols, int x) {
+    return (x + 1) * cols / kNumXcd - x * cols / kNumXcd;
+}
+
 __device__ __forceinline__ WgCoord decode_wg(const AttnArgs& a) {
-    int r = xcd_remap((int)blockIdx.x, (int)gridDim.x);
     WgCoord c;
+    c.valid = true;
+    c.split = 0;
+    if (a.layer_order) {
+        // Layer work order. The hardware hands workgroup b to XCD b % 8, so
+        // XCD x runs workgroups x, x+8, x+16, ... in that order. XCD x owns
+        // the contiguous (head, q-block) columns [x*C/8, (x+1)*C/8) and walks
+        // them for every frame, last frame (longest key range) first: the
+        // q-blocks and frames of one head, which all read that head's keys
+        // from key 0 upward, share one L2, and the longest work starts first.
+        const int cols = a.heads * a.nqb;
+        const int x = (int)blockIdx.x % kNumXcd;
+        const int j = (int)blockIdx.x / kNumXcd;
+        const int n = xcd_columns(cols, x);
+        if (n == 0 || j >= n * a.frames) {
+            c.valid = false;
+            c.qb = c.head = c.frame = 0;
+            return c;
+        }
+        const int col = x * cols / kNumXcd + j % n;
+        c.frame = a.frames - 1 - j / n;
+        c.head = col / a.nqb;
+        c.qb = col % a.nqb;
+        return c;
+    }
+    int r = xcd_remap((int)blockIdx.x, (int)gridDim.x);
     c.qb = r % a.nqb;
     r /= a.nqb;
     c.split = r % a.splits;
@@ -113,6 +151,17 @@ __device__ __forceinline__ WgCoord decode_wg(const AttnArgs& a) {
     c.head = r % a.heads;
     c.frame = r / a.heads;
     return c;
+}
+
+// Key range [kbeg, kend) of a workgroup: its frame's range, then its split.
+__device__ __forceinline__ void wg_keys(const AttnArgs& a, const WgCoord& c, long& kbeg,
+                                        long& kend) {
+    const long e = a.key_end + (long)c.frame * a.kend_step;
+    long b = e - a.max_span;
+    if (b < a.key_begin) b = a.key_begin;
+    kbeg = b + (long)c.split * a.keys_per_split;
+    kend = kbeg + a.keys_per_split;
+    if (kend > e) kend = e;
 }
 
 // Value of x held by lane (lane ^ 32).
@@ -294,7 +343,12 @@ __device__ __forceinline__ void lgkm_wait_tr(u32x2& a, u32x2& b, u32x2& c, u32x2
 // chunks XOR-swizzled by row & 15) and stored as full rows, 16 bytes per
 // lane, instead of 8-byte pieces scattered over 32 rows. `stage` is 8 KiB of
 // LDS that no other wave touches any more.
-template <typename T>
+// An fp16 partial row is stored as P * 2^e with e chosen per query row so
+// that its largest magnitude lies in [2^14, 2^15): every element keeps fp16's
+// 11-bit precision relative to the row maximum whatever the scale of V (no
+// overflow above 65504, no subnormal partials for tiny V); e goes to
+// part_exp and the combine undoes it exactly.
+template <typename T, bool kScaled>
 __device__ __forceinline__ void store_rows_staged(const AttnArgs& a, const WgCoord& c, int wave,
                                                   int lane, const f32x16 (&o)[4], float m_run,
                                                   float l_run, unsigned char* stage) {
@@ -303,13 +357,28 @@ __device__ __forceinline__ void store_rows_staged(const AttnArgs& a, const WgCoo
     const int hh = lane >> 5;
     const int q0 = c.qb * kBlockQ + wave * 32;
     const float inv_l = 1.0f / l_run;
+    int e = 0;
+    if constexpr (kScaled) {
+        float mx = 0.f;
+#pragma unroll
+        for (int nb = 0; nb < 4; ++nb)
+#pragma unroll
+            for (int v = 0; v < 16; ++v) mx = fmaxf(mx, fabsf(o[nb][v]));
+        mx = fmaxf(mx, other_half(mx)) * inv_l;
+        if (mx > 0.f && mx <= 3.0e38f) e = 14 - ilogbf(mx);
+    }
+    auto cvt = [&](float x) -> T {
+        const float y = x * inv_l;
+        if constexpr (kScaled) return (T)__builtin_amdgcn_ldexpf(y, e);
+        return (T)y;
+    };
     unsigned char* wrow = stage + lq * 256;
 #pragma unroll
     for (int nb = 0; nb < 4; ++nb) {
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
-            const t4 w = {(T)(o[nb][4 * g + 0] * inv_l), (T)(o[nb][4 * g + 1] * inv_l),
-                          (T)(o[nb][4 * g + 2] * inv_l), (T)(o[nb][4 * g + 3] * inv_l)};
+            const t4 w = {cvt(o[nb][4 * g + 0]), cvt(o[nb][4 * g + 1]), cvt(o[nb][4 * g + 2]),
+                          cvt(o[nb][4 * g + 3])};
             const int pc = (4 * nb + g) ^ (lq & 15);
             *reinterpret_cast<t4*>(wrow + 16 * pc + 8 * hh) = w;
         }
@@ -328,8 +397,11 @@ __device__ __forceinline__ void store_rows_staged(const AttnArgs& a, const WgCoo
         if (q < a.nq) *reinterpret_cast<u32x4*>(base + (long)q * a.D + 8 * lc) = v;
     }
     const int q = q0 + lq;
-    if (split && hh == 0 && q < a.nq)
-        a.part_lse[(slab * a.heads + c.head) * (long)a.nq + q] = m_run + __log2f(l_run);
+    if (split && hh == 0 && q < a.nq) {
+        const long i = (slab * a.heads + c.head) * (long)a.nq + q;
+        a.part_lse[i] = m_run + __log2f(l_run);
+        a.part_exp[i] = (float)e;
+    }
 }
 
 // kMap: the launch reads a KVMap (a.kvmap != null); the map-free variant has
@@ -345,21 +417,26 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_bf16_kernel(AttnArgs a) 
     __shared__ __attribute__((aligned(256))) unsigned char m_lds[2 * 4 * 256];
 
     const WgCoord c = decode_wg(a);
+    if (!c.valid) return;  // whole workgroup: past the end of the layer order
     const int tid = threadIdx.x;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int lane = tid & 63;
     const int lq = lane & 31;
     const int hh = lane >> 5;
+    // A wave whose 32 queries all lie past nq (the tail q-block of a frame)
+    // only issues its share of the tile copies and joins the barriers.
+    const bool active = c.qb * kBlockQ + wave * 32 < a.nq;
 
-    const long kbeg = a.key_begin + (long)c.split * a.keys_per_split;
-    long kend = kbeg + a.keys_per_split;
-    if (kend > a.key_end) kend = a.key_end;
+    long kbeg, kend;
+    wg_keys(a, c, kbeg, kend);
     const int ntiles = (int)((kend - kbeg + kBf16BlockKeys - 1) / kBf16BlockKeys);
 
     const __bf16* Q = reinterpret_cast<const __bf16*>(a.q) + (long)c.frame * a.q_fstride;
     const unsigned char* Kb = reinterpret_cast<const unsigned char*>(a.k) + 2L * c.frame * a.kv_fstride;
     const unsigned char* Vb = reinterpret_cast<const unsigned char*>(a.v) + 2L * c.frame * a.kv_fstride;
-    const unsigned char* Ab = reinterpret_cast<const unsigned char*>(a.arena);
+    const unsigned char* Ab =
+        kMap ? reinterpret_cast<const unsigned char*>(a.arena) + (long)c.frame * a.arena_fstride
+             : nullptr;
     const long* map = kMap ? a.kvmap + (long)c.frame * a.map_fstride : nullptr;
     const long row_bytes = 2L * a.D;
     const long hoff_b = 2L * c.head * kHeadDim;
@@ -407,6 +484,9 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_bf16_kernel(AttnArgs a) 
     // offsets from the arena base: an entry m is used when its row ends
     // within 4 GiB of that base (2*(m+1)*row_bytes <= 2^32); any negative
     // entry, or one beyond that, reads the original K/V row (offset ~0u).
+    // Rows at or past the range end take the original-row path too, whose
+    // descriptor reads them as zeros (their map words are zero-filled
+    // padding, not entries).
     const unsigned m_wave = (unsigned)(uintptr_t)m_lds + 256u * wave;
     const unsigned max_arena_row = 0x80000000u / rb - 1u;
     unsigned mdec[4];
@@ -417,11 +497,15 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_bf16_kernel(AttnArgs a) 
         wait_vm<0>();
         const unsigned ad = m_wave + 1024u * (unsigned)(t & 1) + 8u * (unsigned)(lane >> 4);
         u32x2 m0 = lds_b64<0>(ad), m1 = lds_b64<32>(ad), m2 = lds_b64<64>(ad), m3 = lds_b64<96>(ad);
+        const long left = kend - (kbeg + (long)t * kBf16BlockKeys);
+        const int valid_rows = left < kBf16BlockKeys ? (int)left : kBf16BlockKeys;
         lgkm_wait_tr(m0, m1, m2, m3);
         const u32x2 mw[4] = {m0, m1, m2, m3};
 #pragma unroll
         for (int i = 0; i < 4; ++i)
-            mdec[i] = (mw[i][1] == 0u && mw[i][0] <= max_arena_row) ? 2u * mw[i][0] * rb : ~0u;
+            mdec[i] = (ld_row0 + 4 * i < valid_rows && mw[i][1] == 0u && mw[i][0] <= max_arena_row)
+                          ? 2u * mw[i][0] * rb
+                          : ~0u;
     };
     auto load_map = [&](int t) {
         if constexpr (!kMap) return;
@@ -692,13 +776,19 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_bf16_kernel(AttnArgs a) 
             for (int i = 0; i < 4; ++i) mdec[i] = ~0u;
         }
         prep_tile(t + 1, knext, vnext);
-        compute_tile(t, kcur, vcur, [&](int ks) {
-            if ((ks & 1) == 0) copy_pair(ks >> 1);
-        });
+        if (active) {
+            compute_tile(t, kcur, vcur, [&](int ks) {
+                if ((ks & 1) == 0) copy_pair(ks >> 1);
+            });
+        } else {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) copy_pair(i);
+        }
         wg_barrier();
     }
     // the trailing copies land before the workgroup's LDS is released
     wait_vm<0>();
+    if (!active) return;
 
     // Stage in the last tile's stage: every wave has passed the barrier that
     // closed its last read, and the trailing copies target the other stage.
@@ -706,9 +796,9 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_bf16_kernel(AttnArgs a) 
     unsigned char* last_v = (ntiles > 0 && ((ntiles - 1) & 1)) ? v_lds1 : v_lds0;
     unsigned char* stage = (wave < 2 ? last_k : last_v) + 8192 * (wave & 1);
     if (a.splits > 1)
-        store_rows_staged<_Float16>(a, c, wave, lane, o, m_run, l_run, stage);
+        store_rows_staged<_Float16, true>(a, c, wave, lane, o, m_run, l_run, stage);
     else
-        store_rows_staged<OutT>(a, c, wave, lane, o, m_run, l_run, stage);
+        store_rows_staged<OutT, false>(a, c, wave, lane, o, m_run, l_run, stage);
 }
 
 // ---------------------------------------------------------------------------
@@ -723,20 +813,25 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_f32_kernel(AttnArgs a) {
     float* vs_lds = lds + kF32TileFloats;
 
     const WgCoord c = decode_wg(a);
+    if (!c.valid) return;  // whole workgroup: past the end of the layer order
     const int tid = threadIdx.x;
     const int wave = tid >> 6;
     const int lane = tid & 63;
     const int lq = lane & 31;
     const int hh = lane >> 5;
+    // waves with no valid query load their share of each tile, skip the MFMAs
+    const bool active = c.qb * kBlockQ + wave * 32 < a.nq;
 
-    const long kbeg = a.key_begin + (long)c.split * a.keys_per_split;
-    long kend = kbeg + a.keys_per_split;
-    if (kend > a.key_end) kend = a.key_end;
+    long kbeg, kend;
+    wg_keys(a, c, kbeg, kend);
 
     const float* Q = reinterpret_cast<const float*>(a.q) + (long)c.frame * a.q_fstride;
     const float* K = reinterpret_cast<const float*>(a.k) + (long)c.frame * a.kv_fstride;
     const float* V = reinterpret_cast<const float*>(a.v) + (long)c.frame * a.kv_fstride;
-    const float* A = reinterpret_cast<const float*>(a.arena);
+    const float* A = a.arena ? reinterpret_cast<const float*>(
+                                   reinterpret_cast<const unsigned char*>(a.arena) +
+                                   (long)c.frame * a.arena_fstride)
+                             : nullptr;
     const long* map = a.kvmap ? a.kvmap + (long)c.frame * a.map_fstride : nullptr;
     const int hoff = c.head * kHeadDim;
     const long D = a.D;
@@ -796,6 +891,10 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_f32_kernel(AttnArgs a) {
         store_tile();
         __syncthreads();
         if (t0 + kF32BlockKeys < kend) load_tile(t0 + kF32BlockKeys);
+        if (!active) {
+            __syncthreads();
+            continue;
+        }
 
         f32x16 st;
 #pragma unroll
@@ -855,13 +954,15 @@ __device__ __forceinline__ void combine_block(const AttnArgs& a, long block) {
     const int frame = (int)(rq / a.nq);
     const int head = (8 * c8) / kHeadDim;
 
-    float lse[MAXS];
+    float lse[MAXS], pe[MAXS];
     f32x4 p0[MAXS], p1[MAXS];
 #pragma unroll
     for (int s = 0; s < MAXS; ++s) {
         if (s < a.splits) {
             const long slab = (long)s * a.frames + frame;
-            lse[s] = a.part_lse[(slab * a.heads + head) * (long)a.nq + q];
+            const long li = (slab * a.heads + head) * (long)a.nq + q;
+            lse[s] = a.part_lse[li];
+            pe[s] = sizeof(OutT) == 4 ? 0.f : a.part_exp[li];
             const long pofs = (slab * a.nq + q) * (long)a.D + 8 * c8;
             if constexpr (sizeof(OutT) == 4) {
                 const float* po = static_cast<const float*>(a.part_o) + pofs;
@@ -879,10 +980,16 @@ __device__ __forceinline__ void combine_block(const AttnArgs& a, long block) {
             }
         }
     }
-    float mx = lse[0];
+    // Partial s holds P_s * 2^e_s. With e0 = min_s e_s the result is
+    // 2^-e0 * sum_s w_s 2^(e0 - e_s) (P_s 2^e_s) / sum_s w_s: every factor
+    // 2^(e0 - e_s) <= 1, and 2^-e0 is applied once at the end.
+    float mx = lse[0], e0 = pe[0];
 #pragma unroll
     for (int s = 1; s < MAXS; ++s)
-        if (s < a.splits) mx = fmaxf(mx, lse[s]);
+        if (s < a.splits) {
+            mx = fmaxf(mx, lse[s]);
+            e0 = fminf(e0, pe[s]);
+        }
     float wsum = 0.f;
     float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -890,14 +997,15 @@ __device__ __forceinline__ void combine_block(const AttnArgs& a, long block) {
         if (s < a.splits) {
             const float w = fast_exp2(lse[s] - mx);
             wsum += w;
+            const float ws = __builtin_amdgcn_ldexpf(w, (int)(e0 - pe[s]));
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                acc[i] = fmaf(w, p0[s][i], acc[i]);
-                acc[4 + i] = fmaf(w, p1[s][i], acc[4 + i]);
+                acc[i] = fmaf(ws, p0[s][i], acc[i]);
+                acc[4 + i] = fmaf(ws, p1[s][i], acc[4 + i]);
             }
         }
     }
-    const float inv = 1.0f / wsum;
+    const float inv = __builtin_amdgcn_ldexpf(1.0f / wsum, -(int)e0);
     OutT* out = reinterpret_cast<OutT*>(a.out) + (long)frame * a.q_fstride + (long)q * a.D + 8 * c8;
     if constexpr (sizeof(OutT) == 4) {
         const f32x4 w0 = {acc[0] * inv, acc[1] * inv, acc[2] * inv, acc[3] * inv};
@@ -917,38 +1025,11 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(AttnArgs a) {
     combine_block<OutT, MAXS>(a, blockIdx.x);
 }
 
-// The combine followed by a staging flush in the same launch: workgroups
-// [0, combine_blocks) merge the partials, the rest run the flush (it may
-// overwrite arena rows and KVMap entries: the attention kernel that read
-// them has completed before this launch starts).
-template <typename OutT, int MAXS>
-__global__ __launch_bounds__(256) void attn_combine_stage_kernel(AttnArgs a, stage::RunArgs r,
-                                                                 int combine_blocks) {
-    const int b = blockIdx.x;
-    if (b < combine_blocks)
-        combine_block<OutT, MAXS>(a, b);
-    else
-        stage::stage_runs_block(r, b - combine_blocks);
-}
-
 template <typename OutT>
-void launch_combine(const AttnArgs& a, hipStream_t st, const stage::RunArgs* follow) {
+void launch_combine(const AttnArgs& a, hipStream_t st) {
     const long total = (long)a.frames * a.nq * (a.D / 8);
-    const long cblocks = (total + 255) / 256;
+    const dim3 grid((unsigned)((total + 255) / 256));
     const dim3 block(256);
-    if (follow) {
-        const dim3 grid((unsigned)(cblocks + stage::run_blocks(*follow)));
-        if (a.splits <= 2)
-            hipLaunchKernelGGL((attn_combine_stage_kernel<OutT, 2>), grid, block, 0, st, a, *follow, (int)cblocks);
-        else if (a.splits <= 4)
-            hipLaunchKernelGGL((attn_combine_stage_kernel<OutT, 4>), grid, block, 0, st, a, *follow, (int)cblocks);
-        else if (a.splits <= 8)
-            hipLaunchKernelGGL((attn_combine_stage_kernel<OutT, 8>), grid, block, 0, st, a, *follow, (int)cblocks);
-        else
-            hipLaunchKernelGGL((attn_combine_stage_kernel<OutT, 16>), grid, block, 0, st, a, *follow, (int)cblocks);
-        return;
-    }
-    const dim3 grid((unsigned)cblocks);
     if (a.splits <= 2)
         hipLaunchKernelGGL((attn_combine_kernel<OutT, 2>), grid, block, 0, st, a);
     else if (a.splits <= 4)
@@ -972,7 +1053,12 @@ struct DeviceInfo {
 
 std::mutex g_mu;
 std::vector<DeviceInfo> g_dev_info;
+// Split-partial workspace, one buffer per (device, stream): launches on one
+// stream reuse its buffer in stream order, launches on different streams
+// never share one. Buffers live until the process ends.
 struct Workspace {
+    int dev = -1;
+    void* stream = nullptr;
     void* ptr = nullptr;
     size_t bytes = 0;
 };
@@ -1004,14 +1090,21 @@ DeviceInfo device_info(int dev) {
     return di;
 }
 
-void* workspace(int dev, size_t bytes) {
+void* workspace(int dev, void* stream, size_t bytes) {
     std::lock_guard<std::mutex> lk(g_mu);
-    if ((int)g_ws.size() <= dev) g_ws.resize(dev + 1);
-    Workspace& w = g_ws[dev];
+    Workspace* wp = nullptr;
+    for (Workspace& w : g_ws)
+        if (w.dev == dev && w.stream == stream) wp = &w;
+    if (!wp) {
+        g_ws.push_back(Workspace{dev, stream, nullptr, 0});
+        wp = &g_ws.back();
+    }
+    Workspace& w = *wp;
     if (w.bytes < bytes) {
-        // Growing waits for in-flight users of the old buffer.
+        // Growing waits for the in-flight users of the old buffer: launches
+        // on this same stream.
         if (w.ptr) {
-            (void)hipDeviceSynchronize();
+            (void)hipStreamSynchronize(static_cast<hipStream_t>(stream));
             (void)hipFree(w.ptr);
             w.ptr = nullptr;
             w.bytes = 0;
@@ -1073,102 +1166,204 @@ LaunchPlan plan_launch(int dtype, int nq, int heads, int frames, long span, cons
 
 }  // namespace
 
-// Core launcher shared by all public attention entry points.
+// Positional form used by the reference-signature entry points: every frame
+// attends the same key range.
 int launch_attention(int dtype, const void* q, const void* k, const void* v, const void* arena,
                      const long* kvmap, void* out, int nq, int D, int heads, int frames,
                      long q_fstride, long kv_fstride, long map_fstride, long key_begin,
                      long key_end, void* stream) {
-    return launch_attention(dtype, q, k, v, arena, kvmap, out, nq, D, heads, frames, q_fstride,
-                            kv_fstride, map_fstride, key_begin, key_end, stream, nullptr);
+    AttnLaunch L;
+    L.dtype = dtype;
+    L.q = q;
+    L.k = k;
+    L.v = v;
+    L.arena = arena;
+    L.kvmap = kvmap;
+    L.out = out;
+    L.nq = nq;
+    L.D = D;
+    L.heads = heads;
+    L.frames = frames;
+    L.q_fstride = q_fstride;
+    L.kv_fstride = kv_fstride;
+    L.map_fstride = map_fstride;
+    L.key_begin = key_begin;
+    L.key_end = key_end;
+    L.stream = stream;
+    return launch_attention(L);
 }
 
-int launch_attention(int dtype, const void* q, const void* k, const void* v, const void* arena,
-                     const long* kvmap, void* out, int nq, int D, int heads, int frames,
-                     long q_fstride, long kv_fstride, long map_fstride, long key_begin,
-                     long key_end, void* stream, const void* follow) {
-    if (dtype != 0 && dtype != 1) {
-        set_error("attention: dtype %d not supported (0 = fp32, 1 = bf16)", dtype);
+namespace {
+
+constexpr long kNoSpanLimit = 0x4000000000000000L;
+
+// Argument checks that need no device. Returns 0 or 1 with the error recorded.
+int validate_launch(const AttnLaunch& L) {
+    if (L.dtype != 0 && L.dtype != 1) {
+        set_error("attention: dtype %d not supported (0 = fp32, 1 = bf16)", L.dtype);
         return 1;
     }
-    if (heads <= 0 || D != heads * kHeadDim) {
-        set_error("attention: head_dim must be 128 (D=%d heads=%d)", D, heads);
+    if (L.heads <= 0 || L.D != L.heads * kHeadDim) {
+        set_error("attention: head_dim must be 128 (D=%d heads=%d)", L.D, L.heads);
         return 1;
     }
-    if (nq <= 0 || frames <= 0) {
-        set_error("attention: empty launch (nq=%d frames=%d)", nq, frames);
+    if (L.nq <= 0 || L.frames <= 0) {
+        set_error("attention: empty launch (nq=%d frames=%d)", L.nq, L.frames);
         return 1;
     }
-    if (key_end <= key_begin || key_begin < 0) {
-        set_error("attention: empty or negative key range [%ld, %ld)", key_begin, key_end);
+    if (L.key_end <= L.key_begin || L.key_begin < 0) {
+        set_error("attention: empty or negative key range [%ld, %ld)", L.key_begin, L.key_end);
         return 1;
     }
-    if (!q || !k || !v || !out) {
+    if (L.kend_step < 0 || L.q_fstride < 0 || L.kv_fstride < 0 || L.map_fstride < 0 ||
+        L.arena_fstride < 0) {
+        set_error("attention: negative frame stride");
+        return 1;
+    }
+    if (L.kend_step != 0 && !L.layer) {
+        set_error("attention: per-frame key ranges need a layer launch");
+        return 1;
+    }
+    if (!L.q || !L.k || !L.v || !L.out) {
         set_error("attention: null q/k/v/out pointer");
         return 1;
     }
-    if (key_end > 0x7fffffffL || (long)frames * kv_fstride / (D > 0 ? D : 1) + key_end > 0x7fffffffL) {
+    const long last = (long)(L.frames - 1);
+    const long max_key_end = L.key_end + last * L.kend_step;
+    if (max_key_end > 0x7fffffffL ||
+        last * L.kv_fstride / L.D + max_key_end > 0x7fffffffL) {
         set_error("attention: key rows must stay below 2^31");
         return 1;
     }
-    if (kvmap && !arena) {
+    if (L.kvmap && !L.arena) {
         set_error("attention: kvmap given without arena");
         return 1;
     }
-    const int align = 16;
-    if (((uintptr_t)q | (uintptr_t)k | (uintptr_t)v | (uintptr_t)out |
-         (uintptr_t)arena) % align) {
+    if (L.arena_fstride % 16) {
+        set_error("attention: arena regions must be 16-byte aligned");
+        return 1;
+    }
+    if (((uintptr_t)L.q | (uintptr_t)L.k | (uintptr_t)L.v | (uintptr_t)L.out |
+         (uintptr_t)L.arena) % 16) {
         set_error("attention: q/k/v/out/arena must be 16-byte aligned");
         return 1;
     }
+    return 0;
+}
+
+// Fills the kernel arguments and the launch shape of a validated launch.
+int prepare_launch(const AttnLaunch& L, const DeviceInfo& di, AttnArgs& a, LaunchPlan& p) {
+    const long max_key_end = L.key_end + (long)(L.frames - 1) * L.kend_step;
+    const long max_span = L.max_span > 0 ? L.max_span : kNoSpanLimit;
+    // longest range of any frame: the last frame's (ranges only grow)
+    long span_last = max_key_end - L.key_begin;
+    if (span_last > max_span) span_last = max_span;
+
+    const int bk = L.dtype == 1 ? kBf16BlockKeys : kF32BlockKeys;
+    if (L.layer) {
+        p.nqb = (L.nq + kBlockQ - 1) / kBlockQ;
+        p.splits = 1;
+        p.keys_per_split = ((span_last + bk - 1) / bk) * bk;
+        const long cols = (long)L.heads * p.nqb;
+        p.grid = (long)kNumXcd * ((cols + kNumXcd - 1) / kNumXcd) * L.frames;
+    } else {
+        p = plan_launch(L.dtype, L.nq, L.heads, L.frames, L.key_end - L.key_begin, di);
+    }
+    if (p.grid > 0x7fffffffL) {
+        set_error("attention: grid too large");
+        return 1;
+    }
+
+    a.q = L.q;
+    a.k = L.k;
+    a.v = L.v;
+    a.arena = L.arena;
+    a.kvmap = L.kvmap;
+    a.out = L.out;
+    a.part_o = nullptr;
+    a.part_lse = nullptr;
+    a.part_exp = nullptr;
+    a.q_fstride = L.q_fstride;
+    a.kv_fstride = L.kv_fstride;
+    a.map_fstride = L.map_fstride;
+    a.arena_fstride = L.arena_fstride;
+    a.key_begin = L.key_begin;
+    a.key_end = L.key_end;
+    a.kend_step = L.kend_step;
+    a.max_span = max_span;
+    a.keys_per_split = p.keys_per_split;
+    a.nq = L.nq;
+    a.D = L.D;
+    a.heads = L.heads;
+    a.frames = L.frames;
+    a.splits = p.splits;
+    a.nqb = p.nqb;
+    a.layer_order = L.layer ? 1 : 0;
+    a.scale_log2 = kLog2e / sqrtf((float)kHeadDim);
+    return 0;
+}
+
+// Workspace of a split launch: partial rows, then the log-sum-exps, then the
+// row-scale exponents, each 256-byte aligned.
+size_t partial_bytes(const AttnArgs& a, int dtype, size_t* lse_offset, size_t* exp_offset) {
+    const size_t po = (size_t)a.splits * a.frames * a.nq * a.D * (dtype == 1 ? 2 : 4);
+    const size_t pl = (size_t)a.splits * a.frames * a.heads * a.nq * sizeof(float);
+    const size_t off = ((po + 255) / 256) * 256;
+    const size_t off2 = off + ((pl + 255) / 256) * 256;
+    if (lse_offset) *lse_offset = off;
+    if (exp_offset) *exp_offset = off2;
+    return off2 + pl;
+}
+
+}  // namespace
+
+size_t attention_workspace_bytes(const AttnLaunch& L) {
+    if (validate_launch(L)) return 0;
+    const int dev = current_device();
+    if (dev < 0) return 0;
+    AttnArgs a;
+    LaunchPlan p;
+    if (prepare_launch(L, device_info(dev), a, p)) return 0;
+    return p.splits > 1 ? partial_bytes(a, L.dtype, nullptr, nullptr) : 0;
+}
+
+// Core launcher shared by all public attention entry points.
+int launch_attention(const AttnLaunch& L) {
+    if (validate_launch(L)) return 1;
     const int dev = current_device();
     if (dev < 0) {
         set_error("attention: no HIP device available");
         return 1;
     }
     const DeviceInfo di = device_info(dev);
-    const long span = key_end - key_begin;
-    LaunchPlan p = plan_launch(dtype, nq, heads, frames, span, di);
-
     AttnArgs a;
-    a.q = q;
-    a.k = k;
-    a.v = v;
-    a.arena = arena;
-    a.kvmap = kvmap;
-    a.out = out;
-    a.part_o = nullptr;
-    a.part_lse = nullptr;
-    a.q_fstride = q_fstride;
-    a.kv_fstride = kv_fstride;
-    a.map_fstride = map_fstride;
-    a.key_begin = key_begin;
-    a.key_end = key_end;
-    a.keys_per_split = p.keys_per_split;
-    a.nq = nq;
-    a.D = D;
-    a.heads = heads;
-    a.frames = frames;
-    a.splits = p.splits;
-    a.nqb = p.nqb;
-    a.scale_log2 = kLog2e / sqrtf((float)kHeadDim);
+    LaunchPlan p;
+    if (prepare_launch(L, di, a, p)) return 1;
 
     if (p.splits > 1) {
-        const size_t po = (size_t)p.splits * frames * nq * D * (dtype == 1 ? 2 : 4);
-        const size_t pl = (size_t)p.splits * frames * heads * nq * sizeof(float);
-        char* ws = static_cast<char*>(workspace(dev, po + pl + 256));
-        if (!ws) {
-            set_error("attention: workspace allocation of %zu bytes failed", po + pl);
-            return 1;
+        size_t lse_off = 0, exp_off = 0;
+        const size_t need = partial_bytes(a, L.dtype, &lse_off, &exp_off);
+        char* ws = nullptr;
+        if (L.workspace) {
+            if (L.workspace_bytes < need) {
+                set_error("attention: workspace of %zu bytes is below the %zu this launch needs",
+                          L.workspace_bytes, need);
+                return 1;
+            }
+            ws = static_cast<char*>(L.workspace);
+        } else {
+            ws = static_cast<char*>(workspace(dev, L.stream, need));
+            if (!ws) {
+                set_error("attention: workspace allocation of %zu bytes failed", need);
+                return 1;
+            }
         }
         a.part_o = ws;
-        a.part_lse = reinterpret_cast<float*>(ws + ((po + 255) / 256) * 256);
+        a.part_lse = reinterpret_cast<float*>(ws + lse_off);
+        a.part_exp = reinterpret_cast<float*>(ws + exp_off);
     }
-    if (p.grid > 0x7fffffffL) {
-        set_error("attention: grid too large");
-        return 1;
-    }
-    hipStream_t st = static_cast<hipStream_t>(stream);
-    if (dtype == 1) {
+    hipStream_t st = static_cast<hipStream_t>(L.stream);
+    if (L.dtype == 1) {
         if (a.kvmap)
             hipLaunchKernelGGL((attn_fwd_bf16_kernel<__bf16, true>), dim3((unsigned)p.grid),
                                dim3(kThreads), 0, st, a);
@@ -1184,19 +1379,17 @@ int launch_attention(int dtype, const void* q, const void* k, const void* v, con
         return 1;
     }
     if (p.splits > 1) {
-        const stage::RunArgs* carried = static_cast<const stage::RunArgs*>(stage_plan_runs(follow));
-        if (dtype == 1)
-            launch_combine<__bf16>(a, st, carried);
+        if (L.dtype == 1)
+            launch_combine<__bf16>(a, st);
         else
-            launch_combine<float>(a, st, carried);
+            launch_combine<float>(a, st);
         e = hipGetLastError();
         if (e != hipSuccess) {
             set_error("attention combine launch: %s", hipGetErrorString(e));
             return 1;
         }
-        if (carried) return 0;
     }
-    return follow ? stage_plan_launch(follow, stream) : 0;
+    return 0;
 }
 
 int attention_splits(int dtype, int nq, int heads, int frames, long span) {

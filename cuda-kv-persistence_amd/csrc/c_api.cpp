@@ -208,6 +208,44 @@ int kvp_attn_forward_range(int dtype, const void* q, const void* k, const void* 
                                  key_begin, key_end, stream);
 }
 
+int kvp_attn_forward_frames(int dtype, const void* q, const void* k, const void* v,
+                            const void* arena, long arena_frame_bytes, const long* kvmap,
+                            long map_frame_stride, void* out, int frames, int T, int D,
+                            int heads, int cross, int window_frames, void* stream) {
+    if (T <= 0 || frames <= 0 || window_frames < 0 || arena_frame_bytes < 0 ||
+        map_frame_stride < 0) {
+        kvp::set_error("attention: bad layer arguments (T=%d frames=%d window=%d)", T, frames,
+                       window_frames);
+        return 1;
+    }
+    kvp::AttnLaunch L;
+    L.dtype = dtype;
+    L.q = q;
+    L.k = k;
+    L.v = v;
+    L.arena = arena;
+    L.kvmap = kvmap;
+    L.out = out;
+    L.nq = T;
+    L.D = D;
+    L.heads = heads;
+    L.frames = frames;
+    L.q_fstride = (long)T * D;
+    L.map_fstride = map_frame_stride;
+    L.arena_fstride = arena_frame_bytes;
+    L.key_begin = 0;
+    L.key_end = T;
+    L.layer = true;
+    L.stream = stream;
+    if (cross) {
+        L.kend_step = T;
+        L.max_span = window_frames > 0 ? (long)window_frames * T : 0;
+    } else {
+        L.kv_fstride = (long)T * D;
+    }
+    return kvp::launch_attention(L);
+}
+
 }  // extern "C"
 
 // C++-linkage reference signatures (reference: src/attn_kernel.h:15-29).

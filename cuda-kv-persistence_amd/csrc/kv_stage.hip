@@ -348,9 +348,7 @@ int kvp_stage_run(void* stager, void* arena, long row_stride_bytes, const KvpRow
 }  // extern "C"
 
 // ---------------------------------------------------------------------------
-// Staging plans: a flush prepared now and launched later, either on its own
-// or as trailing workgroups of another launch (the split combine of the
-// attention launch that precedes it on the stream).
+// Staging plans: a flush prepared now (host bookkeeping) and launched later.
 // ---------------------------------------------------------------------------
 namespace kvp {
 
@@ -392,12 +390,6 @@ void* stage_plan_create(void* stager, void* arena, long row_stride_bytes, const 
         p->slots.assign(map_slots, map_slots + n_map);
     }
     return p;
-}
-
-const void* stage_plan_runs(const void* plan) {
-    const StagePlan* p = static_cast<const StagePlan*>(plan);
-    if (!p || !p->encoded || stage::run_blocks(p->ra) == 0) return nullptr;
-    return &p->ra;
 }
 
 int stage_plan_launch(const void* plan, void* stream) {

@@ -15,6 +15,38 @@ void clear_error();
 // Library stream for the reference-signature attention entry points.
 void* library_stream();
 
+// One attention launch (attn_fwd.hip), frames i = 0..frames-1 of it:
+//   queries  q + i*q_fstride, rows [0, nq); output out + i*q_fstride;
+//   keys     [max(key_begin, e - max_span), e), e = key_end + i*kend_step,
+//            rows indexed against k/v + i*kv_fstride elements;
+//   KVMap    kvmap + i*map_fstride entries, indexed by key row;
+//   arena    arena + i*arena_fstride bytes (0: all frames share one arena).
+// layer = true runs the whole set as one grid in the longest-first XCD
+// column order with no key split (kend_step may then be non-zero; it must be
+// 0 otherwise). max_span <= 0 means no limit. Split partials go to
+// `workspace` when it is given (no allocation; at least
+// attention_workspace_bytes(L) bytes), else to the library's per-(device,
+// stream) buffer.
+struct AttnLaunch {
+    int dtype = 0;  // 0 = fp32, 1 = bf16
+    const void* q = nullptr;
+    const void* k = nullptr;
+    const void* v = nullptr;
+    const void* arena = nullptr;
+    const long* kvmap = nullptr;
+    void* out = nullptr;
+    int nq = 0, D = 0, heads = 0, frames = 1;
+    long q_fstride = 0, kv_fstride = 0, map_fstride = 0, arena_fstride = 0;
+    long key_begin = 0, key_end = 0, kend_step = 0, max_span = 0;
+    bool layer = false;
+    void* stream = nullptr;
+    void* workspace = nullptr;
+    size_t workspace_bytes = 0;
+};
+int launch_attention(const AttnLaunch& L);
+// Split-partial bytes launch_attention(L) needs (0 when it does not split).
+size_t attention_workspace_bytes(const AttnLaunch& L);
+
 // Core attention launch (attn_fwd.hip). Queries q[frame*q_fstride + row*D]
 // for rows [0, nq) of `frames` frames; keys [key_begin, key_end) against
 // k/v bases offset by frame*kv_fstride elements and kvmap offset by
@@ -25,27 +57,14 @@ int launch_attention(int dtype, const void* q, const void* k, const void* v,
                      long kv_fstride, long map_fstride, long key_begin,
                      long key_end, void* stream);
 
-// Same, followed on the stream by a prepared staging flush (see below): the
-// flush runs as trailing workgroups of the split-combine launch when there
-// is one and the flush is argument-encoded, else as its own launch right
-// after the attention launch. follow may be null.
-int launch_attention(int dtype, const void* q, const void* k, const void* v,
-                     const void* arena, const long* kvmap, void* out, int nq,
-                     int D, int heads, int frames, long q_fstride,
-                     long kv_fstride, long map_fstride, long key_begin,
-                     long key_end, void* stream, const void* follow);
-
 int attention_splits(int dtype, int nq, int heads, int frames, long span);
 
 // Staging plans (kv_stage.hip): a flush with the arguments of kvp_stage_run,
-// prepared without launching. stage_plan_launch launches it on its own;
-// stage_plan_runs returns its argument block when it is argument-encoded and
-// not empty (else null), for launches that carry it.
+// prepared without launching; stage_plan_launch launches it.
 void* stage_plan_create(void* stager, void* arena, long row_stride_bytes,
                         const KvpRowCopy* copies, long n_copies, long* map_dev,
                         long map_fill, const long* map_rows,
                         const long* map_slots, long n_map);
-const void* stage_plan_runs(const void* plan);
 int stage_plan_launch(const void* plan, void* stream);
 void stage_plan_free(void* plan);
 

@@ -11,21 +11,25 @@
 //   3. arena_begin_step, KVMap prefix [0, (f+1)*T) reset to -1, then every
 //      selected tile's rows staged in policy order, rows ascending, the map
 //      entry of each staged row set to its arena row / slot;
-//   4. one flush = one launch: every row copy plus the KVMap entries that
-//      change (rows leaving the pinned set -> -1, new or moved rows -> slot);
-//   5. one attention launch for the frame.
-// The device KVMap is never rebuilt from scratch: a host mirror of it gives
-// the exact difference to the map the reference driver would upload for this
-// frame (prefix reset to -1, then the staged rows), so after step 4 the
-// device map holds that map on the whole prefix (and -1 beyond it).
-// Nothing synchronises the host per frame: staging, map updates and
-// attention are ordered on the pipeline's stream. kvp_pipeline_step runs
-// steps 1-5 for one frame in that order; kvp_pipeline_run plans frame f+1
-// before launching frame f and has frame f's attention launch carry frame
-// f+1's staging (as trailing workgroups of its split-combine launch, or as
-// the launch right after it), which saves one launch per frame. The staging
-// of frame f+1 still runs after frame f's attention has read the arena and
-// the map, so device results are those of frame-by-frame stepping.
+//   4. the row copies and the KVMap entries that change, as one launch;
+//   5. attention for the frame.
+//
+// Two ways to run it:
+//   * kvp_pipeline_step(f): frame by frame on one arena, exactly the
+//     reference's sequence; a host mirror of the device KVMap gives the exact
+//     difference to the map the reference driver would upload for the frame
+//     (prefix reset to -1, then the staged rows).
+//   * kvp_pipeline_run: a whole layer in two launches. Steps 1-3 run on the
+//     host for every frame first (a bookkeeping-only manager takes the same
+//     decisions); frame f's arena state goes to its own region of a layer
+//     arena (every mapped row copied to region f at its slot) and frame f's
+//     KVMap to its own slice of a layer map, all in one staging launch; then
+//     one attention launch covers every frame, each reading its own region
+//     and slice. Region f holds, at every slot frame f's map points to, what
+//     the single arena holds at frame f, so the outputs are those of
+//     frame-by-frame stepping, bit for bit.
+// Nothing synchronises the host per frame; all device work is ordered on the
+// pipeline's stream.
 
 #include <algorithm>
 #include <cstring>
@@ -69,12 +73,27 @@ struct Pipeline {
     int next_frame = 0;
     void* stream = nullptr;
 
+    // layer mode (kvp_pipeline_run)
+    std::unique_ptr<KVTileManager> layer_mgr;  // bookkeeping only
+    char* layer_arena = nullptr;               // frames regions of region_bytes
+    long region_rows = 0, region_bytes = 0;
+    long* layer_map = nullptr;                 // frames slices of map_stride entries
+    long map_stride = 0;
+    std::vector<long> layer_mirror;            // device content of layer_map
+    std::vector<std::vector<long>> layer_rows; // per frame: rows mapped on the device
+    std::vector<int> layer_stamp;
+    int layer_step = 0;
+    std::vector<KvpRowCopy> layer_copies;
+    void* layer_stager = nullptr;
+
     ~Pipeline() {
         mgr.reset();
-        if (d_map) {
-            kvp_stream_sync(stream);
-            kvp_dev_free(d_map);
-        }
+        layer_mgr.reset();
+        if (d_map || layer_arena || layer_map || layer_stager) kvp_stream_sync(stream);
+        if (layer_stager) kvp_stager_destroy(layer_stager);
+        if (d_map) kvp_dev_free(d_map);
+        if (layer_arena) kvp_dev_free(layer_arena);
+        if (layer_map) kvp_dev_free(layer_map);
     }
 };
 
@@ -84,11 +103,12 @@ long window_first_frame(const Pipeline& p, int f) {
     return (p.cross && p.window > 0 && f + 1 > p.window) ? f + 1 - p.window : 0;
 }
 
-// Steps 1-4 of a gated frame: selection, streaming release, staging and the
-// KVMap difference, prepared as one staging plan (*plan; launched by the
-// caller, not here). Host bookkeeping only.
-int plan_frame(Pipeline& p, int f, const char* k, const char* v, const float* scores_flat, void** plan) {
-    *plan = nullptr;
+// Steps 1-3 of a gated frame on manager `mgr`: selection, streaming release
+// and staging, leaving the frame's mapped rows in p.map_rows / p.map_slots
+// and its host map in p.h_map. Host bookkeeping only (a manager with a device
+// arena records its copies for the next flush).
+int plan_frame_host(Pipeline& p, KVTileManager& mgr, int f, const char* k, const char* v,
+                    const float* scores_flat) {
     const long T = p.T;
     const long row_bytes = (long)p.D * p.elem;
     if (!scores_flat) {
@@ -97,7 +117,6 @@ int plan_frame(Pipeline& p, int f, const char* k, const char* v, const float* sc
     }
     const long kb_frame = window_first_frame(p, f);
 
-    KVTileManager& mgr = *p.mgr;
     if (f == 0) {
         p.prev_selected.clear();
         if (p.streaming && !mgr.streaming_begin()) {
@@ -149,6 +168,10 @@ int plan_frame(Pipeline& p, int f, const char* k, const char* v, const float* sc
         const long gid = p.ids[i];
         const long src_f = p.cross ? gid / p.num_tiles : f;
         const long tile = p.cross ? gid % p.num_tiles : gid;
+        // uniform hands out ids 0..slots-1 whatever the candidate count; an
+        // id past the last frame names rows outside K/V and stages nothing
+        // (the reference would read past its buffers)
+        if (src_f >= p.frames) continue;
         const long t0 = tile * p.tile_tokens;
         const long c = std::min((long)p.tile_tokens, T - t0);
         bool all = true;
@@ -174,6 +197,17 @@ int plan_frame(Pipeline& p, int f, const char* k, const char* v, const float* sc
         }
         if (all) ++p.staged_tiles;
     }
+    return 0;
+}
+
+// Steps 1-4 of a gated frame in step mode: the host plan, then the row copies
+// and changed map entries prepared as one staging plan (*plan; launched by
+// the caller, not here).
+int plan_frame(Pipeline& p, int f, const char* k, const char* v, const float* scores_flat,
+               void** plan) {
+    *plan = nullptr;
+    KVTileManager& mgr = *p.mgr;
+    if (plan_frame_host(p, mgr, f, k, v, scores_flat)) return 1;
 
     // 4. row copies + changed map entries, as one staging plan
     if (!p.plan_only) {
@@ -209,10 +243,8 @@ int plan_frame(Pipeline& p, int f, const char* k, const char* v, const float* sc
     return 0;
 }
 
-// Step 5: the frame's attention launch, followed on the stream by the
-// staging plan `follow` (may be null).
-int launch_frame(Pipeline& p, int f, const char* q, const char* k, const char* v, char* out,
-                 const void* follow) {
+// Step 5: the frame's attention launch.
+int launch_frame(Pipeline& p, int f, const char* q, const char* k, const char* v, char* out) {
     const long T = p.T;
     const long frame_bytes = T * (long)p.D * p.elem;
     const long kb_frame = window_first_frame(p, f);
@@ -221,20 +253,20 @@ int launch_frame(Pipeline& p, int f, const char* q, const char* k, const char* v
     if (p.cross)
         return kvp::launch_attention(p.dtype, q + f * frame_bytes, k, v, arena, map,
                                      out + f * frame_bytes, p.T, p.D, p.heads, 1, 0, 0, 0,
-                                     kb_frame * T, (long)(f + 1) * T, p.stream, follow);
+                                     kb_frame * T, (long)(f + 1) * T, p.stream);
     return kvp::launch_attention(p.dtype, q + f * frame_bytes, k + f * frame_bytes,
                                  v + f * frame_bytes, arena, map ? map + (long)f * T : nullptr,
-                                 out + f * frame_bytes, p.T, p.D, p.heads, 1, 0, 0, 0, 0, T, p.stream,
-                                 follow);
+                                 out + f * frame_bytes, p.T, p.D, p.heads, 1, 0, 0, 0, 0, T,
+                                 p.stream);
 }
 
 // Step 6: end of the frame's step in the manager.
-void finish_frame(Pipeline& p, int f) {
+void finish_frame(Pipeline& p, KVTileManager& mgr, int f) {
     if (p.streaming)
         p.prev_selected = p.selected;
     else
-        p.mgr->arena_end_step();
-    if (p.streaming && f + 1 == p.frames) p.mgr->streaming_end();
+        mgr.arena_end_step();
+    if (p.streaming && f + 1 == p.frames) mgr.streaming_end();
 }
 
 bool check_data(const Pipeline& p, const char* q, const char* k, const char* v, const char* out) {
@@ -259,28 +291,130 @@ int step_frame(Pipeline& p, int f, const char* q, const char* k, const char* v, 
         p.copy_rows = 0;
         p.next_frame = (f + 1 == p.frames) ? 0 : f + 1;
         if (p.plan_only) return 0;
-        return launch_frame(p, f, q, k, v, out, nullptr);
+        return launch_frame(p, f, q, k, v, out);
     }
     void* plan = nullptr;
     int rc = plan_frame(p, f, k, v, scores_flat, &plan);
     if (rc == 0 && plan) rc = kvp::stage_plan_launch(plan, p.stream);
     kvp::stage_plan_free(plan);
-    if (rc == 0 && !p.plan_only) rc = launch_frame(p, f, q, k, v, out, nullptr);
+    if (rc == 0 && !p.plan_only) rc = launch_frame(p, f, q, k, v, out);
     if (rc) return rc;
-    finish_frame(p, f);
+    finish_frame(p, *p.mgr, f);
     p.next_frame = (f + 1 == p.frames) ? 0 : f + 1;
     return 0;
 }
 
-// All frames, the staging of frame f+1 carried by frame f's attention
-// launch: frame f+1 is planned (host bookkeeping) before frame f's launch,
-// and its copies and map updates run right after frame f's attention on the
-// stream, as trailing workgroups of its split-combine launch when there is
-// one. Device results equal frame-by-frame stepping.
-int run_frames(Pipeline& p, const char* q, const char* k, const char* v, char* out,
-               const float* scores_flat) {
+// Layer-mode device state, created at the first kvp_pipeline_run.
+int layer_setup(Pipeline& p) {
+    if (p.layer_mgr) return 0;
+    const long row_bytes = (long)p.D * p.elem;
+    const size_t stride_floats = (size_t)2 * row_bytes / sizeof(float);
+    p.layer_mgr.reset(new (std::nothrow) KVTileManager((size_t)p.set_aside, (size_t)p.set_aside));
+    if (!p.layer_mgr || !p.layer_mgr->init() ||
+        !p.layer_mgr->arena_attach(nullptr, (size_t)p.set_aside, stride_floats)) {
+        p.layer_mgr.reset();
+        kvp::set_error("pipeline: layer manager init failed");
+        return 1;
+    }
+    p.region_rows = p.set_aside / (2 * row_bytes);
+    p.region_bytes = p.region_rows * 2 * row_bytes;
+    p.map_stride = p.cross ? (long)p.frames * p.T : (long)p.T;
+    const long map_entries = (long)p.frames * p.map_stride;
+    p.layer_arena = static_cast<char*>(
+        kvp_dev_alloc((size_t)std::max<long>(1, p.frames * p.region_bytes)));
+    p.layer_map = static_cast<long*>(kvp_dev_alloc((size_t)map_entries * sizeof(long)));
+    p.layer_stager = kvp_stager_create();
+    if (!p.layer_arena || !p.layer_map || !p.layer_stager) {
+        kvp::set_error("pipeline: layer arena / map allocation failed");
+        return 1;
+    }
+    p.layer_mirror.assign((size_t)map_entries, -1L);
+    p.layer_rows.assign((size_t)p.frames, {});
+    p.layer_stamp.assign((size_t)p.map_stride, 0);
+    // the device map starts as all -1, matching the mirror
+    if (kvp_stage_run(p.layer_stager, nullptr, 0, nullptr, 0, p.layer_map, map_entries, nullptr,
+                      nullptr, 0, p.stream))
+        return 1;
+    return 0;
+}
+
+// Frame f's share of the layer staging launch: every mapped row copied into
+// region f at its slot, and the entries of map slice f that change.
+void layer_collect(Pipeline& p, int f, const char* k, const char* v) {
+    const long row_bytes = (long)p.D * p.elem;
+    const long base = (long)f * p.map_stride;
+    const long rel = p.cross ? 0 : (long)f * p.T;  // intra slices are frame-relative
+    ++p.layer_step;
+    for (size_t i = 0; i < p.map_rows.size(); ++i) {
+        const long r = p.map_rows[i];
+        const long slot = p.map_slots[i];
+        KvpRowCopy c;
+        c.k_src = k + r * row_bytes;
+        c.v_src = v + r * row_bytes;
+        c.dst_row = (long)f * p.region_rows + slot;
+        c.k_bytes = (unsigned)row_bytes;
+        c.v_bytes = (unsigned)row_bytes;
+        p.layer_copies.push_back(c);
+        const long e = r - rel;
+        p.layer_stamp[(size_t)e] = p.layer_step;
+        if (p.layer_mirror[(size_t)(base + e)] != slot) {
+            p.upd_rows.push_back(base + e);
+            p.upd_vals.push_back(slot);
+            p.layer_mirror[(size_t)(base + e)] = slot;
+        }
+    }
+    std::vector<long>& prev = p.layer_rows[(size_t)f];
+    for (long e : prev) {
+        if (p.layer_stamp[(size_t)e] != p.layer_step && p.layer_mirror[(size_t)(base + e)] != -1) {
+            p.upd_rows.push_back(base + e);
+            p.upd_vals.push_back(-1);
+            p.layer_mirror[(size_t)(base + e)] = -1;
+        }
+    }
+    prev.clear();
+    for (long r : p.map_rows) prev.push_back(r - rel);
+}
+
+// One attention launch over all frames of the layer.
+int layer_attention(Pipeline& p, const char* q, const char* k, const char* v, char* out) {
+    kvp::AttnLaunch L;
+    L.dtype = p.dtype;
+    L.q = q;
+    L.k = k;
+    L.v = v;
+    L.out = out;
+    if (p.persist) {
+        L.arena = p.layer_arena;
+        L.kvmap = p.layer_map;
+        L.map_fstride = p.map_stride;
+        L.arena_fstride = p.region_bytes;
+    }
+    L.nq = p.T;
+    L.D = p.D;
+    L.heads = p.heads;
+    L.frames = p.frames;
+    L.q_fstride = (long)p.T * p.D;
+    L.layer = true;
+    L.stream = p.stream;
+    if (p.cross) {
+        L.key_begin = 0;
+        L.key_end = p.T;      // frame 0: [0, T)
+        L.kend_step = p.T;    // frame f: ends at (f + 1) * T
+        L.max_span = p.window > 0 ? (long)p.window * p.T : 0;
+    } else {
+        L.kv_fstride = (long)p.T * p.D;
+        L.key_begin = 0;
+        L.key_end = p.T;
+    }
+    return kvp::launch_attention(L);
+}
+
+// A whole layer: host plans of every frame, one staging launch for all
+// frames' arena regions and map slices, one attention launch.
+int run_layer(Pipeline& p, const char* q, const char* k, const char* v, char* out,
+              const float* scores_flat) {
     p.next_frame = 0;
-    if (!p.persist || p.plan_only) {
+    if (p.plan_only) {
         for (int f = 0; f < p.frames; ++f) {
             const int rc = step_frame(p, f, q, k, v, out, scores_flat);
             if (rc) return rc;
@@ -288,19 +422,28 @@ int run_frames(Pipeline& p, const char* q, const char* k, const char* v, char* o
         return 0;
     }
     if (!check_data(p, q, k, v, out)) return 1;
-    void* plan = nullptr;
-    int rc = plan_frame(p, 0, k, v, scores_flat, &plan);
-    if (rc == 0 && plan) rc = kvp::stage_plan_launch(plan, p.stream);
-    kvp::stage_plan_free(plan);
-    for (int f = 0; rc == 0 && f < p.frames; ++f) {
-        finish_frame(p, f);
-        void* next = nullptr;
-        if (f + 1 < p.frames) rc = plan_frame(p, f + 1, k, v, scores_flat, &next);
-        if (rc == 0) rc = launch_frame(p, f, q, k, v, out, next);
-        kvp::stage_plan_free(next);
+    if (!p.persist) {
+        p.count = 0;
+        p.staged_tiles = 0;
+        p.copy_rows = 0;
+        return layer_attention(p, q, k, v, out);
     }
-    p.next_frame = 0;
-    return rc;
+    if (layer_setup(p)) return 1;
+    p.layer_copies.clear();
+    p.upd_rows.clear();
+    p.upd_vals.clear();
+    for (int f = 0; f < p.frames; ++f) {
+        if (plan_frame_host(p, *p.layer_mgr, f, k, v, scores_flat)) return 1;
+        layer_collect(p, f, k, v);
+        finish_frame(p, *p.layer_mgr, f);
+    }
+    if (!p.layer_copies.empty() || !p.upd_rows.empty()) {
+        if (kvp_stage_run(p.layer_stager, p.layer_arena, 2L * p.D * p.elem, p.layer_copies.data(),
+                          (long)p.layer_copies.size(), p.layer_map, 0, p.upd_rows.data(),
+                          p.upd_vals.data(), (long)p.upd_rows.size(), p.stream))
+            return 1;
+    }
+    return layer_attention(p, q, k, v, out);
 }
 
 }  // namespace
@@ -391,8 +534,8 @@ int kvp_pipeline_step(void* p, int f, const void* q, const void* k, const void* 
 
 int kvp_pipeline_run(void* p, const void* q, const void* k, const void* v, void* out,
                      const float* scores_flat) {
-    return run_frames(*PL(p), static_cast<const char*>(q), static_cast<const char*>(k),
-                      static_cast<const char*>(v), static_cast<char*>(out), scores_flat);
+    return run_layer(*PL(p), static_cast<const char*>(q), static_cast<const char*>(k),
+                     static_cast<const char*>(v), static_cast<char*>(out), scores_flat);
 }
 
 int kvp_pipeline_selected(void* p, long* ids, int cap) {
@@ -419,6 +562,10 @@ void* kvp_pipeline_arena(void* p) {
     return PL(p)->mgr ? PL(p)->mgr->arena_device_ptr() : nullptr;
 }
 const long* kvp_pipeline_device_map(void* p) { return PL(p)->d_map; }
+void* kvp_pipeline_layer_arena(void* p) { return PL(p)->layer_arena; }
+long kvp_pipeline_layer_region_bytes(void* p) { return PL(p)->region_bytes; }
+const long* kvp_pipeline_layer_map(void* p) { return PL(p)->layer_map; }
+long kvp_pipeline_layer_map_stride(void* p) { return PL(p)->map_stride; }
 void* kvp_pipeline_manager(void* p) { return PL(p)->mgr.get(); }
 
 }  // extern "C"

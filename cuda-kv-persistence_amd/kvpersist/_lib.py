@@ -85,6 +85,9 @@ SIGNATURES = {
                                                      c_int, c_int, c_int]),
     "kvp_attn_forward_range": (c_int, [c_int, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
                                        c_void_p, c_int, c_int, c_int, c_long, c_long, c_void_p]),
+    "kvp_attn_forward_frames": (c_int, [c_int, c_void_p, c_void_p, c_void_p, c_void_p, c_long,
+                                        c_void_p, c_long, c_void_p, c_int, c_int, c_int, c_int,
+                                        c_int, c_int, c_void_p]),
     "kvp_set_stream": (None, [c_void_p]),
     "kvp_get_stream": (c_void_p, []),
     "kvp_last_error": (c_char_p, []),
@@ -121,6 +124,10 @@ SIGNATURES = {
     "kvp_pipeline_arena": (c_void_p, [c_void_p]),
     "kvp_pipeline_device_map": (c_void_p, [c_void_p]),
     "kvp_pipeline_manager": (c_void_p, [c_void_p]),
+    "kvp_pipeline_layer_arena": (c_void_p, [c_void_p]),
+    "kvp_pipeline_layer_region_bytes": (c_long, [c_void_p]),
+    "kvp_pipeline_layer_map": (c_void_p, [c_void_p]),
+    "kvp_pipeline_layer_map_stride": (c_long, [c_void_p]),
     # upstream K/V producer (reference: src/backbone.py:8-67), include/kvp_producer.h
     "kvp_layer_norm": (c_int, [c_int, c_int, c_void_p, c_void_p, c_void_p, c_void_p, c_long,
                                c_int, ctypes.c_float, c_void_p]),

@@ -280,6 +280,18 @@ def attn_forward_range(dtype: int, q, k, v, arena, kvmap, out, nq: int, D: int, 
            "attn_forward_range")
 
 
+def attn_forward_frames(dtype: int, q, k, v, arena, kvmap, out, frames: int, T: int, D: int,
+                        heads: int, *, cross: bool, window_frames: int = 0,
+                        arena_frame_bytes: int = 0, map_frame_stride: int = 0,
+                        stream: int | None = None) -> None:
+    """All frames of a layer in one launch (frame f reads arena region f and
+    KVMap slice f); see kvp_attn_forward_frames in kvp_c_api.h."""
+    _check(_lib.load().kvp_attn_forward_frames(dtype, _ptr(q), _ptr(k), _ptr(v), _ptr(arena),
+                                               arena_frame_bytes, _ptr(kvmap), map_frame_stride,
+                                               _ptr(out), frames, T, D, heads, int(cross),
+                                               window_frames, stream), "attn_forward_frames")
+
+
 def attn_splits(dtype: int, nq: int, heads: int, frames: int, span: int) -> int:
     return int(_lib.load().kvp_attn_splits(dtype, nq, heads, frames, span))
 
@@ -337,6 +349,8 @@ class FramePipeline:
                                            self._scores), f"pipeline step {f}")
 
     def run(self, q=None, k=None, v=None, out=None) -> None:
+        """A whole layer: one staging launch for every frame's arena region and
+        KVMap slice, then one attention launch over all frames."""
         _check(self._lib.kvp_pipeline_run(self._h, _ptr(q), _ptr(k), _ptr(v), _ptr(out),
                                           self._scores), "pipeline run")
 
@@ -369,3 +383,18 @@ class FramePipeline:
 
     def device_map_ptr(self) -> int:
         return int(self._lib.kvp_pipeline_device_map(self._h) or 0)
+
+    # layer mode (after run): frame f's arena region and KVMap slice
+    def layer_arena_ptr(self, f: int = 0) -> int:
+        base = int(self._lib.kvp_pipeline_layer_arena(self._h) or 0)
+        return base + f * int(self._lib.kvp_pipeline_layer_region_bytes(self._h)) if base else 0
+
+    def layer_region_bytes(self) -> int:
+        return int(self._lib.kvp_pipeline_layer_region_bytes(self._h))
+
+    def layer_map_ptr(self, f: int = 0) -> int:
+        base = int(self._lib.kvp_pipeline_layer_map(self._h) or 0)
+        return base + 8 * f * int(self._lib.kvp_pipeline_layer_map_stride(self._h)) if base else 0
+
+    def layer_map_stride(self) -> int:
+        return int(self._lib.kvp_pipeline_layer_map_stride(self._h))

@@ -140,6 +140,23 @@ int kvp_attn_forward_range(int dtype, const void* q, const void* k,
                            int heads, long key_begin, long key_end,
                            void* stream);
 
+/* A whole layer in one launch (additive; the reference launches one frame
+ * at a time). q/out: [frames*T, D]; k/v: [frames*T, D] (absolute rows).
+ * Frame f's queries q[f*T .. (f+1)*T) attend
+ *   cross == 0: the keys of frame f, KVMap slice kvmap + f*map_frame_stride
+ *               indexed by frame-relative key (the reference's remap slice);
+ *   cross != 0: keys [max(0, f+1-W)*T, (f+1)*T) (W = window_frames, 0 = the
+ *               whole causal prefix), slice kvmap + f*map_frame_stride indexed
+ *               by absolute key row.
+ * Frame f's arena is arena + f*arena_frame_bytes (0: one shared arena). The
+ * frames run as one grid, longest key range first, with no key split. */
+int kvp_attn_forward_frames(int dtype, const void* q, const void* k,
+                            const void* v, const void* arena,
+                            long arena_frame_bytes, const long* kvmap,
+                            long map_frame_stride, void* out, int frames,
+                            int T, int D, int heads, int cross,
+                            int window_frames, void* stream);
+
 void kvp_set_stream(void* stream);
 void* kvp_get_stream(void);
 const char* kvp_last_error(void);
@@ -203,7 +220,15 @@ int kvp_pipeline_set_stream(void* p, void* stream);
  * (may be NULL for policy none). Returns 0 on success. */
 int kvp_pipeline_step(void* p, int f, const void* q, const void* k,
                       const void* v, void* out, const float* scores_flat);
-/* All frames 0..frames-1 (streaming state is reset first). */
+/* A whole layer, frames 0..frames-1 (streaming state is reset first), in
+ * two launches: every frame's host plan is made first, then one staging
+ * launch writes frame f's arena state to region f of a layer arena (every row
+ * frame f's map points to, at its slot) and frame f's KVMap to slice f of a
+ * layer map, then one attention launch runs all frames, frame f reading its
+ * own region and slice. Outputs equal frame-by-frame stepping bit for bit.
+ * The layer arena is frames x (set_aside rounded down to whole rows) bytes;
+ * the layer map holds frames slices of frames*T (cross) or T (intra)
+ * entries, absolute key rows in cross mode, frame-relative in intra mode. */
 int kvp_pipeline_run(void* p, const void* q, const void* k, const void* v,
                      void* out, const float* scores_flat);
 /* Introspection of the last step. */
@@ -213,9 +238,16 @@ long kvp_pipeline_slots(void* p);
 long kvp_pipeline_staged_tiles(void* p);
 long kvp_pipeline_staged_bytes(void* p);
 long kvp_pipeline_copy_rows(void* p);
+/* Step mode's arena and device KVMap (kvp_pipeline_step). */
 void* kvp_pipeline_arena(void* p);
 const long* kvp_pipeline_device_map(void* p);
 void* kvp_pipeline_manager(void* p);
+/* Layer mode (kvp_pipeline_run): region f at arena + f*region_bytes,
+ * slice f at map + f*map_stride entries; NULL / 0 before the first run. */
+void* kvp_pipeline_layer_arena(void* p);
+long kvp_pipeline_layer_region_bytes(void* p);
+const long* kvp_pipeline_layer_map(void* p);
+long kvp_pipeline_layer_map_stride(void* p);
 
 #ifdef __cplusplus
 }

@@ -231,6 +231,8 @@ def plan_frames(policy: str, *, cross: bool, streaming: bool, frames: int, T: in
         for gid in ids:
             src_f = gid // num_tiles if cross else f
             tile = gid % num_tiles if cross else gid
+            if src_f >= frames:
+                continue  # uniform id past the last frame: rows outside K/V
             t0 = tile * tile_tokens
             c = min(tile_tokens, T - t0)
             ok = True

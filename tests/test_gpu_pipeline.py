@@ -164,13 +164,36 @@ def test_c5_shape_single_frame_pair_bf16():
     assert float((base.float().cpu()[T:T + 128] - want).abs().max()) <= 2e-2
 
 
+def _layer_region(pl, f, rows, dtype):
+    n = rows * 2 * D
+    buf = torch.empty(n, dtype=dtype, device=DEV)
+    esz = 4 if dtype == torch.float32 else 2
+    from kvpersist import _lib
+    lib = _lib.load()
+    torch.cuda.synchronize()
+    assert lib.kvp_memcpy_d2d(buf.data_ptr(), pl.layer_arena_ptr(f), n * esz, None) == 0
+    torch.cuda.synchronize()
+    return buf.view(rows, 2 * D)
+
+
+def _layer_map(pl, f, n):
+    from kvpersist import _lib
+    lib = _lib.load()
+    host = np.empty(n, dtype=np.int64)
+    torch.cuda.synchronize()
+    assert lib.kvp_memcpy_d2h(host.ctypes.data, pl.layer_map_ptr(f), n * 8, None) == 0
+    return host
+
+
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 @pytest.mark.parametrize("streaming", [False, True])
-def test_run_carried_staging_equals_stepping(dtype, streaming):
-    """kvp_pipeline_run plans frame f+1 before launching frame f and lets the
-    attention launch of frame f carry frame f+1's staging. Outputs must equal
-    frame-by-frame stepping bitwise, and after the run the device KVMap and
-    the arena must hold the last frame's state of the oracle driver."""
+def test_run_layer_regions_and_maps_match_oracle_plan(dtype, streaming):
+    """kvp_pipeline_run stages every frame's arena state into its own region
+    and its KVMap into its own slice, then runs all frames in one launch.
+    After the run, slice f must equal the oracle driver's map of frame f and
+    region f must hold [K row | V row] at every slot that map points to;
+    outputs are bitwise equal to policy none run the same way, and within
+    the dtype's bar of frame-by-frame stepping (which may split key ranges)."""
     cfg = workloads.CONFIGS["c3"]
     frames, T = 4, cfg.tokens
     qkv = _device_inputs(frames, T, dtype, seed=9)
@@ -178,27 +201,45 @@ def test_run_carried_staging_equals_stepping(dtype, streaming):
     scores = workloads.motion_for(cfg, 1)[:frames]
     set_aside = cfg.set_aside if dtype == torch.bfloat16 else 2 * cfg.set_aside
     elem = 4 if dtype == torch.float32 else 2
+    d = 0 if dtype == torch.float32 else 1
     stepped = _run_pipeline("motion", cross=True, streaming=streaming, frames=frames, T=T,
                             dtype=dtype, set_aside=set_aside, scores=scores, qkv=qkv)
-    d = 0 if dtype == torch.float32 else 1
-    pl = FramePipeline("motion", cross=True, streaming=streaming, frames=frames, T=T, D=D,
-                       heads=HEADS, tile_tokens=16, set_aside_bytes=set_aside, dtype=d)
-    pl.set_scores(scores)
-    out = torch.empty_like(qd)
-    for _ in range(2):  # a second pass reuses the pipeline's device state
-        pl.run(qd, kd, vd, out)
-        torch.cuda.synchronize()
-        assert torch.equal(out, stepped), streaming
-    plan = mm.plan_frames("motion", cross=True, streaming=streaming, frames=frames, T=T, D=D,
-                          tile_tokens=16, set_aside=set_aside, elem=elem, scores_flat=scores)
-    dmap = _device_map(pl, frames * T)
-    np.testing.assert_array_equal(dmap, plan[frames - 1]["map"])
-    rows = np.nonzero(dmap >= 0)[0]
-    assert rows.size > 0
-    arena = _arena_rows(pl, set_aside // (2 * D * elem), dtype)
-    kflat, vflat = kd.view(frames * T, D), vd.view(frames * T, D)
-    slots = torch.from_numpy(dmap[rows]).to(DEV)
-    ridx = torch.from_numpy(rows).to(DEV)
-    assert torch.equal(arena[slots, :D], kflat[ridx])
-    assert torch.equal(arena[slots, D:], vflat[ridx])
-    pl.close()
+    outs = {}
+    for policy in ("none", "motion"):
+        pl = FramePipeline(policy, cross=True, streaming=streaming, frames=frames, T=T, D=D,
+                           heads=HEADS, tile_tokens=16, set_aside_bytes=set_aside, dtype=d)
+        pl.set_scores(scores)
+        out = torch.empty_like(qd)
+        for rep in range(2):  # a second pass reuses the pipeline's device state
+            out.zero_()
+            pl.run(qd, kd, vd, out)
+            torch.cuda.synchronize()
+            if rep == 0:
+                first = out.clone()
+            else:
+                assert torch.equal(out, first)
+        outs[policy] = out
+        if policy == "motion":
+            plan = mm.plan_frames("motion", cross=True, streaming=streaming, frames=frames, T=T,
+                                  D=D, tile_tokens=16, set_aside=set_aside, elem=elem,
+                                  scores_flat=scores)
+            assert pl.layer_map_stride() == frames * T
+            rows_per_region = set_aside // (2 * D * elem)
+            assert pl.layer_region_bytes() == rows_per_region * 2 * D * elem
+            kflat, vflat = kd.view(frames * T, D), vd.view(frames * T, D)
+            for f in range(frames):
+                dmap = _layer_map(pl, f, frames * T)
+                np.testing.assert_array_equal(dmap[:(f + 1) * T], plan[f]["map"],
+                                              err_msg=f"map slice {f}")
+                assert (dmap[(f + 1) * T:] == -1).all(), f
+                rows = np.nonzero(dmap >= 0)[0]
+                assert rows.size > 0
+                region = _layer_region(pl, f, rows_per_region, dtype)
+                slots = torch.from_numpy(dmap[rows]).to(DEV)
+                ridx = torch.from_numpy(rows).to(DEV)
+                assert torch.equal(region[slots, :D], kflat[ridx]), f
+                assert torch.equal(region[slots, D:], vflat[ridx]), f
+        pl.close()
+    assert torch.equal(outs["motion"], outs["none"])
+    tol = 2e-5 if dtype == torch.float32 else 1.6e-2
+    assert float((outs["motion"].float() - stepped.float()).abs().max()) <= tol
