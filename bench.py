@@ -4,16 +4,26 @@
 Workload "C3", the configuration of the headline metric: Wan2.1-1.3B shape,
 8 frames x 1560 tokens, 12 heads x 128, 30 layers, bf16 Q/K/V ~ N(0,1)
 (drawn on the device, seed 42 + layer), causal cross-frame attention, motion
-scores from a seeded smooth AR(1) field. One step = the whole 30-layer pass:
-for every layer and frame, policy select -> arena staging (one gather
-launch) -> device KVMap rebuild -> one attention launch, all stream-ordered.
+scores from a seeded smooth AR(1) field. One step = the whole 30-layer pass
+of the gated pipeline: per layer, every frame's policy select and arena
+plan on the host, one staging launch (every frame's arena region and KVMap
+slice), one attention launch over all 8 frames; all stream-ordered.
 
 value = ms per query frame of that step (all 30 layers), policy `motion`
-(override with --policy). Also reported, per policy (none/recency/motion):
-pipeline ms/frame and attention-kernel ms/frame; the roofline of the
-dominant kernel (attn_fwd_bf16) from HIP events over its launches; and the
-CPU baseline: the oracle's PyTorch fp32 attention on a bounded sample of the
-same workload on this host's cores.
+(override with --policy, workload with --config c4 / c5).
+
+Reported per policy (none / uniform / recency / motion / reuse_weighted):
+pipeline ms/frame; attention-kernel ms/frame, TFLOP/s and fraction of the
+dense bf16 MFMA peak (HIP events around each layer launch, on the launch
+stream); fabric read bytes per frame of the attention kernel and of all
+library kernels, their delta vs none, and GB/s with the fraction of HBM
+peak. The bytes come from rocprofv3 --pmc child runs of this same script
+(`--profile-policy P`), started before this process touches the GPU; each
+child also runs a 256 MiB device copy whose counter readings calibrate the
+scale of FETCH_SIZE / WRITE_SIZE. `roofline` is the dominant kernel's
+(attn_fwd_bf16, the headline policy's instantiation). `cpu_baseline` is the
+oracle's PyTorch fp32 attention on a bounded sample on this host's cores.
+`c4` / `c5` objects: the other multi-frame configurations, motion policy.
 
 Also reported under "kv_producer": the upstream K/V producer (the reference's
 DiT backbone forward, src/backbone.py:8-67) at the C3 frame set, whole
@@ -23,7 +33,7 @@ flow + per-tile change rates, traces/gen_motion_from_video.py:104-121) over a
 50-frame 832x480 clip, per launch kind, the dominant kernel against the HBM
 roofline.
 
-python bench.py [--steps K] [--warmup W] [--policy P] [--layers L]
+python bench.py [--steps K] [--warmup W] [--policy P] [--config c3|c4|c5]
 """
 
 from __future__ import annotations
@@ -77,7 +87,46 @@ def parse():
     ap.add_argument("--copy-calibration", action="store_true",
                     help="run 4 device-to-device copies of 256 MiB and exit (known-size "
                          "reference for FETCH_SIZE / WRITE_SIZE scaling)")
+    ap.add_argument("--config", default="c3", choices=("c3", "c4", "c5"),
+                    help="headline workload (default c3, the metric's configuration)")
+    ap.add_argument("--calibrate", action="store_true",
+                    help="with --profile-policy: end with the 256 MiB calibration copies")
+    ap.add_argument("--no-counters", action="store_true",
+                    help="skip the rocprofv3 --pmc child runs (fabric bytes per policy)")
+    ap.add_argument("--no-legs", action="store_true", help="skip the c4 / c5 legs")
+    ap.add_argument("--cold-rows-nt", action="store_true",
+                    help="KVMap launches load original (non-arena) K/V rows non-temporally")
+    ap.add_argument("--counter-timeout", type=int, default=240,
+                    help="seconds allowed per rocprofv3 child run")
     return ap.parse_args()
+
+
+def host_cpu():
+    """(logical CPUs visible to this process, CPU model name)."""
+    model = "unknown"
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    try:
+        n = len(os.sched_getaffinity(0))
+    except AttributeError:
+        n = os.cpu_count() or 1
+    return n, model
+
+
+def cpu_threads():
+    """Threads for the CPU baselines: the CPUs this process may use, capped by
+    OMP_NUM_THREADS when set (the GPU box sets it to its 16-CPU share)."""
+    n, _ = host_cpu()
+    try:
+        n = min(n, int(os.environ.get("OMP_NUM_THREADS", n)))
+    except ValueError:
+        pass
+    return max(1, n)
 
 
 def cpu_baseline(cfg, units_target: int):
@@ -86,7 +135,7 @@ def cpu_baseline(cfg, units_target: int):
     import torch
     sys.path.insert(0, str(ROOT))
     from oracle import attention as at
-    nthreads = min(16, os.cpu_count() or 1)
+    nthreads = cpu_threads()
     torch.set_num_threads(nthreads)
     T, D, H = cfg.tokens, 1536, 12
     rng = np.random.default_rng(42)
@@ -107,8 +156,9 @@ def cpu_baseline(cfg, units_target: int):
     per_unit_s = sorted(times)[1] / units
     # C3: 36 frame-units per layer, 30 layers, 8 query frames
     ms_per_frame = per_unit_s * cfg.frame_units() * cfg.layers / cfg.frames * 1e3
+    nproc, model = host_cpu()
     return {"value": round(ms_per_frame, 3), "unit": "ms/frame", "cores": nthreads,
-            "kind": "port",
+            "host_nproc": nproc, "cpu_model": model, "kind": "port",
             "sample": f"oracle fp32 torch-CPU attention, 1 layer, query frames 0..{frames - 1} "
                       f"causal ({units} frame-units of 1560x1560x12x128), median of 3, "
                       f"extrapolated x{cfg.frame_units()}/{units} units x {cfg.layers} layers "
@@ -243,7 +293,7 @@ def producer_cpu_baseline(model, cfg, frames, layers):
     import torch
     sys.path.insert(0, str(ROOT))
     from oracle import backbone as ob
-    nthreads = min(16, os.cpu_count() or 1)
+    nthreads = cpu_threads()
     torch.set_num_threads(nthreads)
     p = {n: model.get_param(n).numpy() for n in model.param_names()
          if n.startswith("blocks.0.")}
@@ -381,28 +431,170 @@ def motion_cpu_baseline(frames):
                       f"(the reference's cv2 path is not in this image)"}
 
 
+POLICIES = ("none", "uniform", "recency", "motion", "reuse_weighted")
+ATTN_KERNEL = "attn_fwd_bf16_kernel"
+STAGE_KERNELS = ("stage_kernel", "stage_runs_kernel", "map_fill_kernel", "attn_combine")
+COPY_KERNEL = "__amd_rocclr_copyBuffer"
+CALIB_BYTES = 256 << 20
+CALIB_COPIES = 4
+
+
+def counter_run(counters, policy, args, workdir):
+    """One rocprofv3 --pmc pass over `bench.py --profile-policy policy` (one
+    step of that policy's pipeline plus the copy calibration) in a fresh
+    child process; returns {counter: {kernel class: [per-dispatch value]}}
+    (FETCH_SIZE / WRITE_SIZE in KiB)."""
+    import csv
+    import glob
+    import subprocess
+    d = Path(workdir) / f"{'_'.join(counters)}_{policy}"
+    cmd = ["rocprofv3", "--pmc", *counters, "--output-format", "csv", "-d", str(d), "-o", "p",
+           "--", sys.executable, str(ROOT / "bench.py"), "--profile-policy", policy,
+           "--config", args.config, "--layers", str(args.layers), "--steps", "1",
+           "--calibrate"]
+    if args.set_aside_tiles is not None:
+        cmd += ["--set-aside-tiles", str(args.set_aside_tiles)]
+    if args.cold_rows_nt:
+        cmd.append("--cold-rows-nt")
+    if args.streaming:
+        cmd.append("--streaming")
+    env = dict(os.environ, TMPDIR=os.environ.get("TMPDIR", "/tmp"))
+    proc = subprocess.Popen(cmd, cwd="/tmp", env=env, stdout=subprocess.DEVNULL,
+                            stderr=subprocess.DEVNULL, start_new_session=True)
+    tag = f"rocprofv3 {' '.join(counters)} {policy}"
+    try:
+        rc = proc.wait(timeout=args.counter_timeout)
+    except subprocess.TimeoutExpired:
+        os.killpg(proc.pid, 9)
+        proc.wait()
+        raise RuntimeError(f"{tag}: over {args.counter_timeout} s")
+    per = {c: {} for c in counters}
+    names = {}
+    for f in glob.glob(str(d / "**" / "*counter_collection.csv"), recursive=True):
+        with open(f) as fh:
+            for r in csv.DictReader(fh):
+                c = r["Counter_Name"]
+                if c not in per:
+                    continue
+                key = int(r["Dispatch_Id"])
+                per[c][key] = per[c].get(key, 0.0) + float(r["Counter_Value"])
+                names[key] = r["Kernel_Name"]
+    if not names:
+        raise RuntimeError(f"{tag}: no counter rows (exit {rc})")
+    res = {}
+    for c in counters:
+        out = {"attention": [], "staging": [], "copy": []}
+        for key in sorted(per[c]):
+            n = names[key]
+            if ATTN_KERNEL in n:
+                out["attention"].append(per[c][key])
+            elif any(k in n for k in STAGE_KERNELS):
+                out["staging"].append(per[c][key])
+            elif COPY_KERNEL in n:
+                out["copy"].append(per[c][key])
+        res[c] = out
+    if "FETCH_SIZE" in res or "WRITE_SIZE" in res:
+        c0 = "FETCH_SIZE" if "FETCH_SIZE" in res else "WRITE_SIZE"
+        big = [x for x in res[c0]["copy"] if x * 1024 >= CALIB_BYTES / 8]
+        if len(big) != CALIB_COPIES:
+            raise RuntimeError(f"{tag}: {len(big)} calibration copies")
+        res[c0]["copy"] = big
+    return res
+
+
+def measure_counters(args, cfg, headline):
+    """Fabric bytes per policy from rocprofv3 child runs (FETCH_SIZE for every
+    policy, WRITE_SIZE for the headline policy), each scaled by the reading of
+    the 256 MiB calibration copies of its own run."""
+    import shutil
+    import tempfile
+    if not shutil.which("rocprofv3"):
+        return {"error": "rocprofv3 not found"}
+    t0 = time.perf_counter()
+    frames_total = args.layers * cfg.frames
+    res = {"counter_runs": [], "policies": {}}
+    with tempfile.TemporaryDirectory(prefix="kvp_bench_") as work:
+        for pol in POLICIES:
+            r = counter_run(["FETCH_SIZE"], pol, args, work)["FETCH_SIZE"]
+            factor = CALIB_BYTES / (sorted(r["copy"])[1] * 1024.0)
+            attn = sum(r["attention"]) * 1024.0 * factor
+            stage = sum(r["staging"]) * 1024.0 * factor
+            res["policies"][pol] = {
+                "attn_read_bytes_per_frame": round(attn / frames_total),
+                "all_kernels_read_bytes_per_frame": round((attn + stage) / frames_total),
+                "attn_launches": len(r["attention"]), "fetch_factor": round(factor, 4)}
+            res["counter_runs"].append(f"FETCH_SIZE {pol}")
+            log(f"counters: {pol} attention reads {attn / frames_total / 1e9:.4f} GB/frame "
+                f"(calibration x{factor:.3f})")
+        w = counter_run(["WRITE_SIZE"], headline, args, work)["WRITE_SIZE"]
+        wfactor = CALIB_BYTES / (sorted(w["copy"])[1] * 1024.0)
+        res["policies"][headline]["attn_write_bytes_per_frame"] = round(
+            sum(w["attention"]) * 1024.0 * wfactor / frames_total)
+        res["policies"][headline]["write_factor"] = round(wfactor, 4)
+        res["counter_runs"].append(f"WRITE_SIZE {headline}")
+        for pol in ("none", headline):
+            h = counter_run(["TCC_HIT_sum", "TCC_MISS_sum"], pol, args, work)
+            hit, miss = sum(h["TCC_HIT_sum"]["attention"]), sum(h["TCC_MISS_sum"]["attention"])
+            res["policies"][pol]["attn_l2_hit_rate"] = round(hit / max(1.0, hit + miss), 4)
+            res["counter_runs"].append(f"TCC_HIT_sum TCC_MISS_sum {pol}")
+    base = res["policies"]["none"]
+    for pol, rec in res["policies"].items():
+        rec["attn_read_delta_vs_none"] = round(
+            rec["attn_read_bytes_per_frame"] / base["attn_read_bytes_per_frame"] - 1.0, 5)
+        rec["all_kernels_read_delta_vs_none"] = round(
+            rec["all_kernels_read_bytes_per_frame"] / base["all_kernels_read_bytes_per_frame"]
+            - 1.0, 5)
+    res["seconds"] = round(time.perf_counter() - t0, 1)
+    return res
+
+
+def compulsory_read_bytes_per_frame(cfg):
+    """Algorithmic read bytes of the layer launch per query frame: the launch
+    reads every frame's Q rows once and, since every key row of the layer is
+    in some frame's range, every K and V row once: 3 x T x D bf16 per frame."""
+    return 3 * cfg.tokens * 1536 * 2
+
+
 def main():
     args = parse()
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU only; --gpus must be 1 "
                                    "(multi-GPU sharding is a design note, not a code path)"}))
         sys.exit(2)
-    import numpy as np
+    sys.path.insert(0, str(ROOT / "cuda-kv-persistence_amd"))
+    from kvpersist import workloads
+    cfg = workloads.CONFIGS[args.config]
+    counters = None
+    child = args.profile_policy or args.copy_calibration or args.motion_only or args.producer_only
+    if not child and not args.no_counters:
+        # before this process initialises the GPU: the children are separate
+        # processes under rocprofv3
+        log("fabric-byte counters (rocprofv3 child runs) ...")
+        try:
+            counters = measure_counters(args, cfg, args.policy)
+        except RuntimeError as e:
+            counters = {"error": str(e)}
+            log(f"counters failed: {e}")
+
     import torch
-    from kvpersist import FramePipeline, _lib, api, workloads
+    from kvpersist import FramePipeline, _lib, api
 
     lib = _lib.load()
     assert torch.cuda.is_available(), "bench needs a GPU"
     dev = torch.device("cuda:0")
-    if args.copy_calibration:
-        nbytes = 256 << 20
-        src = torch.ones(nbytes // 4, device=dev)
+
+    def calibration_copies():
+        src = torch.ones(CALIB_BYTES // 4, device=dev)
         dst = torch.empty_like(src)
         torch.cuda.synchronize()
-        for _ in range(4):
-            assert lib.kvp_memcpy_d2d(dst.data_ptr(), src.data_ptr(), nbytes, None) == 0
+        for _ in range(CALIB_COPIES):
+            assert lib.kvp_memcpy_d2d(dst.data_ptr(), src.data_ptr(), CALIB_BYTES, None) == 0
         torch.cuda.synchronize()
-        print(json.dumps({"copy_calibration_bytes_per_copy": nbytes, "copies": 4}), flush=True)
+
+    if args.copy_calibration:
+        calibration_copies()
+        print(json.dumps({"copy_calibration_bytes_per_copy": CALIB_BYTES,
+                          "copies": CALIB_COPIES}), flush=True)
         return
     if args.motion_only:
         mot = motion_bench(args, torch, torch.cuda.current_stream().cuda_stream)
@@ -412,148 +604,182 @@ def main():
         prod = producer_bench(args, torch, torch.cuda.current_stream().cuda_stream)
         print(json.dumps({"kv_producer": prod}), flush=True)
         return
-    cfg = workloads.CONFIGS["c3"]
     layers = args.layers
-    T, D, H, F = cfg.tokens, workloads.HIDDEN, workloads.HEADS, cfg.frames
     props = torch.cuda.get_device_properties(dev)
     log(f"device {props.name} CUs={props.multi_processor_count} layers={layers}")
+    stream = torch.cuda.current_stream().cuda_stream
 
-    qs, ks, vs, outs = [], [], [], []
-    for layer in range(layers):
-        q, k, v = workloads.qkv_device(F, T, seed=42 + layer, dtype=torch.bfloat16, device="cuda")
-        qs.append(q), ks.append(k), vs.append(v), outs.append(torch.empty_like(q))
-    scores = [workloads.motion_for(cfg, layer) for layer in range(layers)]
-    torch.cuda.synchronize()
-    log("inputs resident")
-
-    # one arena tile = 16 token rows of [K row | V row] in bf16
-    set_aside = (cfg.set_aside if args.set_aside_tiles is None
-                 else args.set_aside_tiles * 16 * 2 * D * 2)
-
-    def make(policy):
-        return FramePipeline(policy, cross=True, streaming=args.streaming, frames=F, T=T, D=D,
-                             heads=H, tile_tokens=16, set_aside_bytes=set_aside,
-                             dtype=api.BF16)
-
-    def run_step(pl):
+    def workload(c):
+        T, D, H, F = c.tokens, workloads.HIDDEN, workloads.HEADS, c.frames
+        data = []
         for layer in range(layers):
-            pl.set_scores(scores[layer])
-            pl.run(qs[layer], ks[layer], vs[layer], outs[layer])
+            q, k, v = workloads.qkv_device(F, T, seed=42 + layer, dtype=torch.bfloat16,
+                                           device="cuda")
+            data.append((q, k, v, torch.empty_like(q), workloads.motion_for(c, layer)))
+        torch.cuda.synchronize()
+        return data
 
-    def timed(pl, steps):
+    def make(c, policy, set_aside):
+        pl = FramePipeline(policy, cross=True, streaming=args.streaming, frames=c.frames,
+                           T=c.tokens, D=workloads.HIDDEN, heads=workloads.HEADS,
+                           tile_tokens=workloads.TILE_TOKENS, set_aside_bytes=set_aside,
+                           dtype=api.BF16, window_frames=c.window)
+        pl.set_stream(stream)
+        pl.set_cold_rows_nt(args.cold_rows_nt)
+        return pl
+
+    def run_step(pl, data):
+        for q, k, v, out, sc in data:
+            pl.set_scores(sc)
+            pl.run(q, k, v, out)
+
+    def timed(pl, data, steps):
         torch.cuda.synchronize()
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         t0 = time.perf_counter()
         e0.record()
         for _ in range(steps):
-            run_step(pl)
+            run_step(pl, data)
         e1.record()
         torch.cuda.synchronize()
         wall = (time.perf_counter() - t0) * 1e3
         return e0.elapsed_time(e1) / steps, wall / steps
 
+    def attn_pass(c, pl, data, gated):
+        """HIP events around every layer's attention launch (the kernel the
+        pipeline runs, on its stream), with the policy's own arena regions and
+        KVMap slices as its last step left them; returns ms per layer."""
+        T, D, H, F = c.tokens, workloads.HIDDEN, workloads.HEADS, c.frames
+        arena = pl.layer_arena_ptr() if gated else None
+        kvmap = pl.layer_map_ptr() if gated else None
+        rb = pl.layer_region_bytes() if gated else 0
+        ms = pl.layer_map_stride() if gated else 0
+        evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+               for _ in data]
+        scratch = torch.empty_like(data[0][3])
+        for rep in range(2):  # the first pass warms, the second is measured
+            for (q, k, v, _, _), (a, b) in zip(data, evs):
+                a.record()
+                api.attn_forward_frames(api.BF16, q, k, v, arena, kvmap, scratch, F, T, D, H,
+                                        cross=True, window_frames=c.window,
+                                        arena_frame_bytes=rb, map_frame_stride=ms,
+                                        cold_rows_nt=args.cold_rows_nt and gated,
+                                        stream=stream)
+                b.record()
+            torch.cuda.synchronize()
+        return sum(a.elapsed_time(b) for a, b in evs) / len(evs)
+
+    set_aside = (cfg.set_aside if args.set_aside_tiles is None
+                 else args.set_aside_tiles * workloads.BF16_TILE_BYTES)
+    data = workload(cfg)
+    log(f"inputs resident ({args.config})")
+
     if args.profile_policy:
-        # one step (what the rocprofv3 passes count); --steps > 1 also times
-        # steps 2.. with HIP events (meaningful only outside the profiler)
-        pl = make(args.profile_policy)
+        # one step (what the rocprofv3 passes count), then the calibration
+        # copies; --steps > 1 also times steps 2.. (outside the profiler only)
+        pl = make(cfg, args.profile_policy, set_aside)
+        run_step(pl, data)
         torch.cuda.synchronize()
-        run_step(pl)
-        torch.cuda.synchronize()
-        rec = {"profile_policy": args.profile_policy, "set_aside_bytes": set_aside,
-               "staged_tiles_last_frame": pl.staged_tiles(), "layers": layers, "frames": F,
-               "query_frames": layers * F}
+        rec = {"profile_policy": args.profile_policy, "config": args.config,
+               "set_aside_bytes": set_aside, "staged_tiles_last_frame": pl.staged_tiles(),
+               "layers": layers, "frames": cfg.frames, "query_frames": layers * cfg.frames}
         if args.steps > 1:
-            ms, _ = timed(pl, args.steps - 1)
-            rec["ms_per_frame"] = round(ms / F, 4)
+            ms, _ = timed(pl, data, args.steps - 1)
+            rec["ms_per_frame"] = round(ms / cfg.frames, 4)
         pl.close()
+        if args.calibrate:
+            calibration_copies()
         print(json.dumps(rec), flush=True)
         return
 
-    # --- headline: policy pipeline, K timed steps -----------------------------------
-    main_pl = make(args.policy)
+    # --- headline: the policy pipeline, K timed steps ----------------------------------
+    F = cfg.frames
+    main_pl = make(cfg, args.policy, set_aside)
     for _ in range(args.warmup):
-        run_step(main_pl)
+        run_step(main_pl, data)
     torch.cuda.synchronize()
     log(f"warmup done ({args.warmup} steps)")
-    ms_step, wall_step = timed(main_pl, args.steps)
+    ms_step, wall_step = timed(main_pl, data, args.steps)
     log(f"policy {args.policy}: {ms_step:.3f} ms/step")
 
-    # --- attention kernel alone: HIP events around each frame's launch ---------------
-    # One launch per (layer, frame) with the policy's own arena and KVMap as the
-    # pipeline left them after its last step (none: no map, the map-free kernel
-    # instantiation), so each policy's figure times the kernel its pipeline runs.
-    # The events are recorded on the stream the launches go to.
-    stream = torch.cuda.current_stream().cuda_stream
-
-    def attn_pass(arena_ptr, map_ptr):
-        api.set_stream(stream)
-        evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-               for _ in range(layers * F)]
-        for rep in range(2):  # first pass warms, second is measured
-            i = 0
-            for layer in range(layers):
-                for f in range(F):
-                    a, b = evs[i]
-                    a.record()
-                    api.attn_forward_single_frame_bf16(qs[layer][f * T:(f + 1) * T], ks[layer],
-                                                       vs[layer], arena_ptr, map_ptr,
-                                                       outs[layer][f * T:(f + 1) * T], T, D, H,
-                                                       1, f)
-                    b.record()
-                    i += 1
-            torch.cuda.synchronize()
-        api.set_stream(None)
-        return sum(a.elapsed_time(b) for a, b in evs)
-
-    # --- per-policy pipeline timing, bitwise gate, attention-only pass -----------------
+    # --- per policy: pipeline timing, bitwise gate, attention kernel alone ------------
+    fl_layer = cfg.flops_per_layer()
+    comp_frame = compulsory_read_bytes_per_frame(cfg)
     policies = {}
-    attn_ms_by_policy = {}
     ref_out = None
-    for pol in ("none", "recency", "motion"):
-        pl = main_pl if pol == args.policy else make(pol)
-        run_step(pl)
-        t, _ = timed(pl, max(1, min(2, args.steps)))
-        o0 = outs[0].clone()
+    for pol in POLICIES:
+        pl = main_pl if pol == args.policy else make(cfg, pol, set_aside)
+        run_step(pl, data)
+        t, _ = timed(pl, data, max(1, min(2, args.steps)))
+        o0 = data[0][3].clone()
         if ref_out is None:
             ref_out = o0
-        policies[pol] = {"pipeline_ms_per_frame": round(t / F, 4),
-                         "bitwise_equal_to_none": bool(torch.equal(o0, ref_out))}
-        arena_ptr, map_ptr = (pl.arena_ptr() or None), (pl.device_map_ptr() or None)
-        ms = attn_pass(arena_ptr if map_ptr else None, map_ptr if arena_ptr else None)
-        attn_ms_by_policy[pol] = ms
-        policies[pol]["attn_kernel_ms_per_frame"] = round(ms / F, 4)
-        policies[pol]["attn_kernel_reads_kvmap"] = bool(arena_ptr and map_ptr)
+        lay_ms = attn_pass(cfg, pl, data, pol != "none")
+        tf = fl_layer / (lay_ms * 1e-3) / 1e12
+        rec = {"pipeline_ms_per_frame": round(t / F, 4),
+               "bitwise_equal_to_none": bool(torch.equal(o0, ref_out)),
+               "attn_kernel_ms_per_frame": round(lay_ms * layers / F, 4),
+               "attn_kernel_ms_per_layer_launch": round(lay_ms, 5),
+               "attn_tflops": round(tf, 2), "attn_mfma_frac": round(tf / BF16_PEAK_TFLOPS, 4),
+               "attn_kernel_reads_kvmap": pol != "none",
+               "staged_tiles_last_frame": pl.staged_tiles()}
+        c = (counters or {}).get("policies", {}).get(pol)
+        if c:
+            rec.update(c)
+            gbs = c["attn_read_bytes_per_frame"] * F / (lay_ms * 1e-3) / 1e9
+            rec["attn_read_gbs"] = round(gbs, 1)
+            rec["attn_hbm_frac"] = round(gbs / HBM_PEAK_GBS, 4)
+            rec["attn_read_vs_compulsory"] = round(c["attn_read_bytes_per_frame"] / comp_frame, 4)
+        policies[pol] = rec
         if pl is not main_pl:
             pl.close()
-        log(f"policy {pol}: {t / F:.4f} ms/frame, attention alone {ms / F:.4f} ms/frame")
+        log(f"policy {pol}: {t / F:.4f} ms/frame, attention alone {lay_ms * layers / F:.4f} "
+            f"ms/frame ({tf:.0f} TFLOP/s)")
 
-    # --- attention kernel roofline: the headline policy's attention-only pass --------
-    fl_layer = cfg.flops_per_layer()
-    attn_ms = attn_ms_by_policy[args.policy]
-    launches = layers * F
-    flops_total = fl_layer * layers
-    achieved = flops_total / (attn_ms * 1e-3) / 1e12
-    log(f"attention kernels ({args.policy}): {attn_ms:.3f} ms over {launches} launches, "
-        f"{achieved:.1f} TFLOP/s")
-
-    # Fabric bytes come from rocprofv3 FETCH_SIZE / WRITE_SIZE runs of this same
-    # workload (bench.py --profile-policy P), scaled by a copy-kernel calibration
-    # and committed under profiles/; counters cannot be read from inside a run.
+    head = policies[args.policy]
+    lay_ms = head["attn_kernel_ms_per_layer_launch"]
+    achieved = fl_layer / (lay_ms * 1e-3) / 1e12
     traffic = None
-    tfile = ROOT / "profiles" / "attn_bf16_c3_traffic.json"
-    if tfile.exists():
-        try:
-            tj = json.loads(tfile.read_text())
-            traffic = tj.get("policies", {}).get(args.policy, {}).get(
-                "attn_hbm_bytes_per_launch", tj.get("hbm_bytes_per_launch"))
-            for pol, rec in tj.get("policies", {}).items():
-                if pol in policies:
-                    policies[pol]["attn_read_bytes_per_frame"] = rec.get("attn_read_bytes_per_frame")
-                    policies[pol]["attn_read_delta_vs_none"] = rec.get("attn_read_delta_vs_none")
-                    policies[pol]["all_kernels_read_bytes_per_frame"] = rec.get(
-                        "all_kernels_read_bytes_per_frame")
-        except (OSError, ValueError):
-            traffic = None
+    if head.get("attn_write_bytes_per_frame") is not None:
+        traffic = round((head["attn_read_bytes_per_frame"] + head["attn_write_bytes_per_frame"])
+                        * F)
+
+    # --- other multi-frame configurations (motion policy) --------------------------
+    legs = {}
+    if not args.no_legs:
+        for name in ("c3", "c4", "c5"):
+            if name == args.config:
+                continue
+            c = workloads.CONFIGS[name]
+            data_leg = workload(c)
+            pl = make(c, "motion", c.set_aside)
+            run_step(pl, data_leg)
+            t, _ = timed(pl, data_leg, 2)
+            lm = attn_pass(c, pl, data_leg, True)
+            tfl = c.flops_per_layer() / (lm * 1e-3) / 1e12
+            nb = FramePipeline("none", cross=True, streaming=False, frames=c.frames,
+                               T=c.tokens, D=workloads.HIDDEN, heads=workloads.HEADS,
+                               dtype=api.BF16, window_frames=c.window)
+            nb.set_stream(stream)
+            o_motion = data_leg[0][3].clone()
+            q, k, v, out, _ = data_leg[0]
+            nb.run(q, k, v, out)
+            torch.cuda.synchronize()
+            legs[name] = {
+                "workload": f"{name}: {c.frames} frames x {c.tokens} tokens, 12 x 128, "
+                            f"{layers} layers, bf16, causal"
+                            + (f", window {c.window} frames" if c.window else "")
+                            + ", motion policy, arena 22 tiles",
+                "pipeline_ms_per_frame": round(t / c.frames, 4),
+                "attn_kernel_ms_per_frame": round(lm * layers / c.frames, 4),
+                "attn_tflops": round(tfl, 2), "attn_mfma_frac": round(tfl / BF16_PEAK_TFLOPS, 4),
+                "attn_launches_per_layer": 1, "key_splits": 1,
+                "bitwise_equal_to_none_layer0": bool(torch.equal(o_motion, out))}
+            nb.close()
+            pl.close()
+            del data_leg
+            torch.cuda.empty_cache()
+            log(f"leg {name}: {t / c.frames:.4f} ms/frame, {tfl:.0f} TFLOP/s")
 
     cpu = None
     if not args.no_cpu_baseline:
@@ -584,29 +810,39 @@ def main():
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "bf16",
-        "data": "synthetic (device N(0,1) Q/K/V, seeded smooth AR(1) motion field)",
+        "data": "synthetic (device N(0,1) Q/K/V, seeded motion field)",
         "config": {
-            "workload": "c3: causal cross-frame attention, 8 frames x 1560 tokens (30x52), "
-                        "12 heads x 128, 30 layers, bf16, KVMap arena 22 tiles (2,162,688 B)",
-            "policy": args.policy, "streaming": bool(args.streaming), "frames": F,
-            "tokens_per_frame": T, "heads": H, "head_dim": 128, "layers": layers,
-            "parallelism": "single GPU",
+            "workload": f"{args.config}: causal cross-frame attention, {F} frames x "
+                        f"{cfg.tokens} tokens, 12 heads x 128, {layers} layers, bf16, "
+                        + (f"window {cfg.window} frames, " if cfg.window else "")
+                        + f"KVMap arena {set_aside // workloads.BF16_TILE_BYTES} tiles "
+                          f"({set_aside:,} B)",
+            "policy": args.policy, "streaming": bool(args.streaming),
+            "cold_rows_nt": bool(args.cold_rows_nt), "frames": F,
+            "tokens_per_frame": cfg.tokens, "heads": workloads.HEADS, "head_dim": 128,
+            "layers": layers, "parallelism": "single GPU",
         },
         "roofline": {
             "bound": "mfma",
-            "kernel": ("attn_fwd_bf16_kernel, KVMap instantiation (+ split combine)"
-                       if policies[args.policy]["attn_kernel_reads_kvmap"]
-                       else "attn_fwd_bf16_kernel, map-free instantiation (+ split combine)"),
+            "kernel": ("attn_fwd_bf16_kernel, " +
+                       ("KVMap instantiation" if head["attn_kernel_reads_kvmap"]
+                        else "map-free instantiation") +
+                       f", one launch per layer ({F} frames)"),
             "achieved": round(achieved, 2),
             "peak": BF16_PEAK_TFLOPS,
             "unit": "TFLOP/s",
             "frac": round(achieved / BF16_PEAK_TFLOPS, 4),
             "traffic": traffic,
-            "flops_per_launch": round(flops_total / launches),
-            "avg_launch_ms": round(attn_ms / launches, 5),
+            "flops_per_launch": round(fl_layer),
+            "avg_launch_ms": lay_ms,
+            "compulsory_read_bytes_per_launch": round(comp_frame * F),
+            "compulsory_write_bytes_per_launch": round(F * cfg.tokens * 1536 * 2),
         },
         "cpu_baseline": cpu,
         "policies": policies,
+        "counters": ({k: v for k, v in counters.items() if k != "policies"}
+                     if counters else None),
+        "legs": legs,
         "wall_ms_per_step": round(wall_step, 3),
         "kv_producer": prod,
         "motion_producer": mot,

@@ -406,8 +406,14 @@ __device__ __forceinline__ void store_rows_staged(const AttnArgs& a, const WgCoo
 
 // kMap: the launch reads a KVMap (a.kvmap != null); the map-free variant has
 // no per-row source selection in its copy path.
-template <typename OutT, bool kMap>
+// kColdNt (KVMap launches only): rows read from the original K/V buffers
+// (not from the arena) are loaded non-temporally (the nt cache-policy bit),
+// so the L2 evicts them first and keeps the arena's lines: the counterpart of
+// the reference's access-policy window, whose misses stream
+// (src/kv_tile_manager.cu:39-47, missProp = cudaAccessPropertyStreaming).
+template <typename OutT, bool kMap, bool kColdNt>
 __global__ __launch_bounds__(kThreads, 2) void attn_fwd_bf16_kernel(AttnArgs a) {
+    constexpr int kColdAux = kColdNt ? 2 : 0;  // buffer-load aux: bit 1 = nt
     __shared__ __attribute__((aligned(1024))) unsigned char k_lds0[kBf16TileBytes];
     __shared__ __attribute__((aligned(1024))) unsigned char v_lds0[kBf16TileBytes];
     __shared__ __attribute__((aligned(1024))) unsigned char k_lds1[kBf16TileBytes];
@@ -549,8 +555,10 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_bf16_kernel(AttnArgs a) 
             __builtin_amdgcn_raw_ptr_buffer_load_lds(arena_rs, kd, 16, ao + kofs[i], 0, 0, 0);
             __builtin_amdgcn_raw_ptr_buffer_load_lds(arena_rs, vd, 16, ao + rb + vofs, 0, 0, 0);
         } else {
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(krs, kd, 16, row_off + kofs[i], 0, 0, 0);
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(vrs, vd, 16, row_off + vofs, 0, 0, 0);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(krs, kd, 16, row_off + kofs[i], 0, 0,
+                                                     kColdAux);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(vrs, vd, 16, row_off + vofs, 0, 0,
+                                                     kColdAux);
         }
     };
 
@@ -1079,7 +1087,8 @@ DeviceInfo device_info(int dev) {
         if (hipGetDeviceProperties(&prop, dev) == hipSuccess) di.cus = prop.multiProcessorCount;
         int nb = 0;
         if (hipOccupancyMaxActiveBlocksPerMultiprocessor(
-                &nb, attn_fwd_bf16_kernel<__bf16, true>, kThreads, 0) == hipSuccess && nb > 0)
+                &nb, attn_fwd_bf16_kernel<__bf16, true, false>, kThreads, 0) == hipSuccess &&
+            nb > 0)
             di.wg_per_cu_bf16 = nb;
         nb = 0;
         if (hipOccupancyMaxActiveBlocksPerMultiprocessor(
@@ -1364,12 +1373,15 @@ int launch_attention(const AttnLaunch& L) {
     }
     hipStream_t st = static_cast<hipStream_t>(L.stream);
     if (L.dtype == 1) {
-        if (a.kvmap)
-            hipLaunchKernelGGL((attn_fwd_bf16_kernel<__bf16, true>), dim3((unsigned)p.grid),
-                               dim3(kThreads), 0, st, a);
+        if (a.kvmap && L.cold_rows_nt)
+            hipLaunchKernelGGL((attn_fwd_bf16_kernel<__bf16, true, true>),
+                               dim3((unsigned)p.grid), dim3(kThreads), 0, st, a);
+        else if (a.kvmap)
+            hipLaunchKernelGGL((attn_fwd_bf16_kernel<__bf16, true, false>),
+                               dim3((unsigned)p.grid), dim3(kThreads), 0, st, a);
         else
-            hipLaunchKernelGGL((attn_fwd_bf16_kernel<__bf16, false>), dim3((unsigned)p.grid),
-                               dim3(kThreads), 0, st, a);
+            hipLaunchKernelGGL((attn_fwd_bf16_kernel<__bf16, false, false>),
+                               dim3((unsigned)p.grid), dim3(kThreads), 0, st, a);
     } else {
         hipLaunchKernelGGL(attn_fwd_f32_kernel, dim3((unsigned)p.grid), dim3(kThreads), 0, st, a);
     }

@@ -211,7 +211,7 @@ int kvp_attn_forward_range(int dtype, const void* q, const void* k, const void* 
 int kvp_attn_forward_frames(int dtype, const void* q, const void* k, const void* v,
                             const void* arena, long arena_frame_bytes, const long* kvmap,
                             long map_frame_stride, void* out, int frames, int T, int D,
-                            int heads, int cross, int window_frames, void* stream) {
+                            int heads, int cross, int window_frames, int flags, void* stream) {
     if (T <= 0 || frames <= 0 || window_frames < 0 || arena_frame_bytes < 0 ||
         map_frame_stride < 0) {
         kvp::set_error("attention: bad layer arguments (T=%d frames=%d window=%d)", T, frames,
@@ -236,6 +236,7 @@ int kvp_attn_forward_frames(int dtype, const void* q, const void* k, const void*
     L.key_begin = 0;
     L.key_end = T;
     L.layer = true;
+    L.cold_rows_nt = (flags & KVP_ATTN_COLD_ROWS_NT) != 0;
     L.stream = stream;
     if (cross) {
         L.kend_step = T;

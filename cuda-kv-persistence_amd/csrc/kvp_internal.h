@@ -39,6 +39,7 @@ struct AttnLaunch {
     long q_fstride = 0, kv_fstride = 0, map_fstride = 0, arena_fstride = 0;
     long key_begin = 0, key_end = 0, kend_step = 0, max_span = 0;
     bool layer = false;
+    bool cold_rows_nt = false;  // bf16 KVMap launches: original rows loaded non-temporally
     void* stream = nullptr;
     void* workspace = nullptr;
     size_t workspace_bytes = 0;

@@ -72,6 +72,7 @@ struct Pipeline {
     long copy_rows = 0;
     int next_frame = 0;
     void* stream = nullptr;
+    bool cold_rows_nt = false;
 
     // layer mode (kvp_pipeline_run)
     std::unique_ptr<KVTileManager> layer_mgr;  // bookkeeping only
@@ -247,17 +248,30 @@ int plan_frame(Pipeline& p, int f, const char* k, const char* v, const float* sc
 int launch_frame(Pipeline& p, int f, const char* q, const char* k, const char* v, char* out) {
     const long T = p.T;
     const long frame_bytes = T * (long)p.D * p.elem;
-    const long kb_frame = window_first_frame(p, f);
-    const void* arena = p.persist ? p.mgr->arena_device_ptr() : nullptr;
-    const long* map = p.persist ? p.d_map : nullptr;
-    if (p.cross)
-        return kvp::launch_attention(p.dtype, q + f * frame_bytes, k, v, arena, map,
-                                     out + f * frame_bytes, p.T, p.D, p.heads, 1, 0, 0, 0,
-                                     kb_frame * T, (long)(f + 1) * T, p.stream);
-    return kvp::launch_attention(p.dtype, q + f * frame_bytes, k + f * frame_bytes,
-                                 v + f * frame_bytes, arena, map ? map + (long)f * T : nullptr,
-                                 out + f * frame_bytes, p.T, p.D, p.heads, 1, 0, 0, 0, 0, T,
-                                 p.stream);
+    kvp::AttnLaunch L;
+    L.dtype = p.dtype;
+    L.q = q + f * frame_bytes;
+    L.out = out + f * frame_bytes;
+    L.arena = p.persist ? p.mgr->arena_device_ptr() : nullptr;
+    L.kvmap = p.persist ? p.d_map : nullptr;
+    L.nq = p.T;
+    L.D = p.D;
+    L.heads = p.heads;
+    L.cold_rows_nt = p.cold_rows_nt;
+    L.stream = p.stream;
+    if (p.cross) {
+        L.k = k;
+        L.v = v;
+        L.key_begin = window_first_frame(p, f) * T;
+        L.key_end = (long)(f + 1) * T;
+    } else {
+        L.k = k + f * frame_bytes;
+        L.v = v + f * frame_bytes;
+        if (L.kvmap) L.kvmap += (long)f * T;
+        L.key_begin = 0;
+        L.key_end = T;
+    }
+    return kvp::launch_attention(L);
 }
 
 // Step 6: end of the frame's step in the manager.
@@ -395,6 +409,7 @@ int layer_attention(Pipeline& p, const char* q, const char* k, const char* v, ch
     L.frames = p.frames;
     L.q_fstride = (long)p.T * p.D;
     L.layer = true;
+    L.cold_rows_nt = p.cold_rows_nt;
     L.stream = p.stream;
     if (p.cross) {
         L.key_begin = 0;
@@ -518,6 +533,11 @@ void kvp_pipeline_destroy(void* p) { delete PL(p); }
 int kvp_pipeline_set_stream(void* p, void* stream) {
     PL(p)->stream = stream;
     if (PL(p)->mgr) PL(p)->mgr->set_stream(stream);
+    return 0;
+}
+
+int kvp_pipeline_set_cold_rows_nt(void* p, int on) {
+    PL(p)->cold_rows_nt = on != 0;
     return 0;
 }
 

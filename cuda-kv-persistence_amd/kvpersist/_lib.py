@@ -87,7 +87,7 @@ SIGNATURES = {
                                        c_void_p, c_int, c_int, c_int, c_long, c_long, c_void_p]),
     "kvp_attn_forward_frames": (c_int, [c_int, c_void_p, c_void_p, c_void_p, c_void_p, c_long,
                                         c_void_p, c_long, c_void_p, c_int, c_int, c_int, c_int,
-                                        c_int, c_int, c_void_p]),
+                                        c_int, c_int, c_int, c_void_p]),
     "kvp_set_stream": (None, [c_void_p]),
     "kvp_get_stream": (c_void_p, []),
     "kvp_last_error": (c_char_p, []),
@@ -112,6 +112,7 @@ SIGNATURES = {
                                        c_int, c_long, c_int, c_int, c_int]),
     "kvp_pipeline_destroy": (None, [c_void_p]),
     "kvp_pipeline_set_stream": (c_int, [c_void_p, c_void_p]),
+    "kvp_pipeline_set_cold_rows_nt": (c_int, [c_void_p, c_int]),
     "kvp_pipeline_step": (c_int, [c_void_p, c_int, c_void_p, c_void_p, c_void_p, c_void_p,
                                   c_float_p]),
     "kvp_pipeline_run": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_float_p]),

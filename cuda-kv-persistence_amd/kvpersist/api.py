@@ -26,6 +26,7 @@ from . import _lib
 KVTM_ADMITTED, KVTM_REFUSED_BUDGET, KVTM_INVALID = 1, 0, -1
 FP32, BF16 = 0, 1
 HEAD_DIM = 128
+COLD_ROWS_NT = 1  # kvp_attn_forward_frames flag (KVP_ATTN_COLD_ROWS_NT)
 
 
 def _ptr(x) -> int | None:
@@ -283,13 +284,15 @@ def attn_forward_range(dtype: int, q, k, v, arena, kvmap, out, nq: int, D: int, 
 def attn_forward_frames(dtype: int, q, k, v, arena, kvmap, out, frames: int, T: int, D: int,
                         heads: int, *, cross: bool, window_frames: int = 0,
                         arena_frame_bytes: int = 0, map_frame_stride: int = 0,
-                        stream: int | None = None) -> None:
+                        cold_rows_nt: bool = False, stream: int | None = None) -> None:
     """All frames of a layer in one launch (frame f reads arena region f and
     KVMap slice f); see kvp_attn_forward_frames in kvp_c_api.h."""
+    flags = COLD_ROWS_NT if cold_rows_nt else 0
     _check(_lib.load().kvp_attn_forward_frames(dtype, _ptr(q), _ptr(k), _ptr(v), _ptr(arena),
                                                arena_frame_bytes, _ptr(kvmap), map_frame_stride,
                                                _ptr(out), frames, T, D, heads, int(cross),
-                                               window_frames, stream), "attn_forward_frames")
+                                               window_frames, flags, stream),
+           "attn_forward_frames")
 
 
 def attn_splits(dtype: int, nq: int, heads: int, frames: int, span: int) -> int:
@@ -343,6 +346,10 @@ class FramePipeline:
 
     def set_stream(self, stream: int | None) -> None:
         self._lib.kvp_pipeline_set_stream(self._h, stream)
+
+    def set_cold_rows_nt(self, on: bool) -> None:
+        """Attention launches load original (non-arena) K/V rows non-temporally."""
+        self._lib.kvp_pipeline_set_cold_rows_nt(self._h, int(bool(on)))
 
     def step(self, f: int, q=None, k=None, v=None, out=None) -> None:
         _check(self._lib.kvp_pipeline_step(self._h, f, _ptr(q), _ptr(k), _ptr(v), _ptr(out),

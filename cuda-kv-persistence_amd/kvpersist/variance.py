@@ -8,8 +8,12 @@ on MI355X with rocprofv3 counters instead of Nsight Compute:
   bf16, one layer (the reference's `policy_experiment` also runs one
   attention launch per frame), synthetic device N(0,1) Q/K/V and the C4
   camera-pan motion field; arena budget 22 bf16 tiles;
-* combos: {dense (arena), stream (sticky slots)} x {none, recency, motion,
-  reuse_weighted} (reference `COMBOS`, :153-155);
+* combos: {dense (arena), stream (sticky slots)} x {none, uniform, recency,
+  motion, reuse_weighted} (the reference's `COMBOS`, :153-155, plus uniform,
+  the fifth policy of its policy file);
+* each frame is one attention launch (kvp_pipeline_step: frame by frame on
+  one arena, the reference driver's sequence), so the launch window below
+  counts frames as the reference's does;
 * each run profiles the attention launches of the run; the window is
   launches SKIP..SKIP+COUNT-1 = 34..49 (reference :39);
 * metric: L2->fabric read bytes per window (`FETCH_SIZE`, KiB, scaled by the
@@ -56,7 +60,7 @@ SKIP, COUNT, REPEATS = 34, 16, 3
 SPREAD_PASS = 0.10
 HOT_RANGE = 0.20
 MODES = ("dense", "stream")
-POLICIES = ("none", "recency", "motion", "reuse_weighted")
+POLICIES = ("none", "uniform", "recency", "motion", "reuse_weighted")
 COMBOS = [(m, p) for m in MODES for p in POLICIES]
 KERNEL = "attn_fwd_bf16_kernel"
 
@@ -156,7 +160,8 @@ def child(mode, policy, out_json):
     else:
         scores = workloads.motion_for(cfg, 0)
     pl.set_scores(scores)
-    pl.run(q, k, v, out)
+    for f in range(F):
+        pl.step(f, q, k, v, out)
     torch.cuda.synchronize()
     digest = hashlib.sha256(out.view(torch.int16).cpu().numpy().tobytes()).hexdigest()
     pl.close()

@@ -149,13 +149,18 @@ int kvp_attn_forward_range(int dtype, const void* q, const void* k,
  *               whole causal prefix), slice kvmap + f*map_frame_stride indexed
  *               by absolute key row.
  * Frame f's arena is arena + f*arena_frame_bytes (0: one shared arena). The
- * frames run as one grid, longest key range first, with no key split. */
+ * frames run as one grid, longest key range first, with no key split.
+ * flags: KVP_ATTN_COLD_ROWS_NT = with a KVMap (bf16), rows read from the
+ * original K/V buffers are loaded non-temporally, so the L2 evicts them
+ * before arena lines (the CDNA4 counterpart of the reference's persisting
+ * window with streaming misses, src/kv_tile_manager.cu:39-47). */
+#define KVP_ATTN_COLD_ROWS_NT 1
 int kvp_attn_forward_frames(int dtype, const void* q, const void* k,
                             const void* v, const void* arena,
                             long arena_frame_bytes, const long* kvmap,
                             long map_frame_stride, void* out, int frames,
                             int T, int D, int heads, int cross,
-                            int window_frames, void* stream);
+                            int window_frames, int flags, void* stream);
 
 void kvp_set_stream(void* stream);
 void* kvp_get_stream(void);
@@ -215,6 +220,9 @@ void* kvp_pipeline_create(const char* policy, int cross, int streaming,
                           int window_frames, int plan_only);
 void kvp_pipeline_destroy(void* p);
 int kvp_pipeline_set_stream(void* p, void* stream);
+/* Residency lever of the pipeline's attention launches: 1 = original K/V
+ * rows non-temporal (KVP_ATTN_COLD_ROWS_NT), 0 = default. */
+int kvp_pipeline_set_cold_rows_nt(void* p, int on);
 /* Run frame f (frames must be stepped in order 0,1,...). q/k/v/out are the
  * full [frames*T, D] buffers; scores_flat is [frames][tiles_per_frame]
  * (may be NULL for policy none). Returns 0 on success. */

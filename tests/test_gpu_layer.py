@@ -101,6 +101,28 @@ def test_layer_launch_matches_oracle_and_map_is_invisible(dtype, mode, window, T
     assert torch.equal(got, base)
 
 
+def test_cold_rows_nt_is_a_cache_hint_only():
+    """Non-temporal loads of original rows change no output bit."""
+    frames, T, heads = 4, 1560, 2
+    q, k, v = _inputs(frames, T, heads, seed=61, dtype=torch.bfloat16)
+    qd, kd, vd = (x.to(DEV).to(torch.bfloat16).contiguous() for x in (q, k, v))
+    rng = np.random.default_rng(61)
+    region_rows = 352
+    arena, kvmap, stride = _layer_arenas(k.to(torch.bfloat16), v.to(torch.bfloat16), frames, T,
+                                         "cross", 0, rng, region_rows)
+    ad, md = arena.to(DEV), kvmap.to(DEV)
+    outs = []
+    for nt in (False, True):
+        out = torch.empty_like(qd)
+        api.attn_forward_frames(api.BF16, qd, kd, vd, ad, md, out, frames, T, heads * 128,
+                                heads, cross=True, arena_frame_bytes=region_rows * 2 * 256 * 2,
+                                map_frame_stride=stride, cold_rows_nt=nt)
+        torch.cuda.synchronize()
+        outs.append(out)
+    assert torch.equal(outs[0], outs[1])
+    assert torch.equal(outs[0], _layer(torch.bfloat16, qd, kd, vd, frames, T, heads, "cross"))
+
+
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 def test_layer_launch_equals_single_frame_launches_within_tolerance(dtype):
     # per-frame launches may split the key range; the layer launch never does
