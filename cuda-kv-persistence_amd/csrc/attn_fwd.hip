@@ -1355,8 +1355,9 @@ int launch_attention(const AttnLaunch& L) {
         char* ws = nullptr;
         if (L.workspace) {
             if (L.workspace_bytes < need) {
-                set_error("attention: workspace of %zu bytes is below the %zu this launch needs",
-                          L.workspace_bytes, need);
+                set_error("attention: this launch needs %zu bytes of split partials, above the "
+                          "%zu-byte workspace it was given",
+                          need, L.workspace_bytes);
                 return 1;
             }
             ws = static_cast<char*>(L.workspace);
@@ -1402,6 +1403,56 @@ int launch_attention(const AttnLaunch& L) {
         }
     }
     return 0;
+}
+
+// ---------------------------------------------------------------------------
+// Allocation-free attention (kvp_attn_forward_range_noalloc): the split
+// partials of a launch go to `scratch`, a fixed device array of this code
+// object, instead of the per-(device, stream) workspace. Every GPU the library
+// runs on holds its own copy from module load until the process ends. Host
+// code never passes the array's name to a kernel (on the host it is only a
+// stand-in for the symbol): the device address is looked up once per device
+// with hipGetSymbolAddress, with that device current, and that address is
+// what the kernels receive. Nothing in the array has to start at zero: the
+// attention kernel writes every partial row, log-sum-exp and row-scale
+// exponent the combine then reads. All calls on one GPU share the array, so
+// calls that overlap on one GPU (two streams, two threads) race.
+// ---------------------------------------------------------------------------
+constexpr size_t kScratchBytes = (size_t)64 << 20;
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+namespace {
+std::mutex g_scratch_mu;
+std::vector<void*> g_scratch_ptr;  // per device; null until looked up
+
+void* scratch_address(int dev) {
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    if ((int)g_scratch_ptr.size() <= dev) g_scratch_ptr.resize(dev + 1, nullptr);
+    if (!g_scratch_ptr[dev]) {
+        void* ptr = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !ptr) {
+            set_error("attention scratch: hipGetSymbolAddress failed: %s", hipGetErrorString(e));
+            return nullptr;
+        }
+        g_scratch_ptr[dev] = ptr;
+    }
+    return g_scratch_ptr[dev];
+}
+}  // namespace
+
+int launch_attention_noalloc(AttnLaunch L) {
+    if (validate_launch(L)) return 1;
+    const int dev = current_device();
+    if (dev < 0) {
+        set_error("attention: no HIP device available");
+        return 1;
+    }
+    void* ptr = scratch_address(dev);
+    if (!ptr) return 1;
+    L.workspace = ptr;
+    L.workspace_bytes = kScratchBytes;
+    return launch_attention(L);
 }
 
 int attention_splits(int dtype, int nq, int heads, int frames, long span) {

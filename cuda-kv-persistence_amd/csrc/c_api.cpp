@@ -208,6 +208,26 @@ int kvp_attn_forward_range(int dtype, const void* q, const void* k, const void* 
                                  key_begin, key_end, stream);
 }
 
+int kvp_attn_forward_range_noalloc(int dtype, const void* q, const void* k, const void* v,
+                                   const void* arena, const long* kvmap, void* out, int nq, int D,
+                                   int heads, long key_begin, long key_end, void* stream) {
+    kvp::AttnLaunch L;
+    L.dtype = dtype;
+    L.q = q;
+    L.k = k;
+    L.v = v;
+    L.arena = arena;
+    L.kvmap = kvmap;
+    L.out = out;
+    L.nq = nq;
+    L.D = D;
+    L.heads = heads;
+    L.key_begin = key_begin;
+    L.key_end = key_end;
+    L.stream = stream;
+    return kvp::launch_attention_noalloc(L);
+}
+
 int kvp_attn_forward_frames(int dtype, const void* q, const void* k, const void* v,
                             const void* arena, long arena_frame_bytes, const long* kvmap,
                             long map_frame_stride, void* out, int frames, int T, int D,

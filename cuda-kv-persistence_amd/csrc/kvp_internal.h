@@ -45,6 +45,10 @@ struct AttnLaunch {
     size_t workspace_bytes = 0;
 };
 int launch_attention(const AttnLaunch& L);
+// launch_attention with the split partials in the library's fixed device
+// scratch array (64 MiB per GPU) instead of an allocated workspace; refuses
+// launches whose partials exceed it. Allocates nothing.
+int launch_attention_noalloc(AttnLaunch L);
 // Split-partial bytes launch_attention(L) needs (0 when it does not split).
 size_t attention_workspace_bytes(const AttnLaunch& L);
 

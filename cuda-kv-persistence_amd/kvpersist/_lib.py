@@ -85,6 +85,9 @@ SIGNATURES = {
                                                      c_int, c_int, c_int]),
     "kvp_attn_forward_range": (c_int, [c_int, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
                                        c_void_p, c_int, c_int, c_int, c_long, c_long, c_void_p]),
+    "kvp_attn_forward_range_noalloc": (c_int, [c_int, c_void_p, c_void_p, c_void_p, c_void_p,
+                                               c_void_p, c_void_p, c_int, c_int, c_int, c_long,
+                                               c_long, c_void_p]),
     "kvp_attn_forward_frames": (c_int, [c_int, c_void_p, c_void_p, c_void_p, c_void_p, c_long,
                                         c_void_p, c_long, c_void_p, c_int, c_int, c_int, c_int,
                                         c_int, c_int, c_int, c_void_p]),

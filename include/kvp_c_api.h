@@ -140,6 +140,21 @@ int kvp_attn_forward_range(int dtype, const void* q, const void* k,
                            int heads, long key_begin, long key_end,
                            void* stream);
 
+/* Allocation-free form of kvp_attn_forward_range, same arguments and
+ * results bit for bit. No counterpart in the reference: it is for callers
+ * that cannot allocate device memory (code under HIP graph capture, tight
+ * serving loops, harnesses that forbid hipMalloc). It calls no hipMalloc,
+ * hipFree or allocating library routine: the split partials of the launch
+ * live in a fixed 64 MiB device array of the library (one per GPU, held
+ * until the process ends), and a launch whose partials exceed it returns 1
+ * with the reason in kvp_last_error(). All calls on one GPU share that array:
+ * calls that overlap on one GPU (other streams, other threads) race. */
+int kvp_attn_forward_range_noalloc(int dtype, const void* q, const void* k,
+                                   const void* v, const void* arena,
+                                   const long* kvmap, void* out, int nq, int D,
+                                   int heads, long key_begin, long key_end,
+                                   void* stream);
+
 /* A whole layer in one launch (additive; the reference launches one frame
  * at a time). q/out: [frames*T, D]; k/v: [frames*T, D] (absolute rows).
  * Frame f's queries q[f*T .. (f+1)*T) attend
