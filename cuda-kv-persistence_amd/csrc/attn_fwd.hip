@@ -35,6 +35,7 @@
 
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cmath>
 #include <cstdint>
 #include <cstdio>
@@ -304,6 +305,17 @@ __device__ __forceinline__ u32x4 lds_b128(unsigned addr) {
 }
 
 template <int OFF>
+__device__ __forceinline__ unsigned lds_b32(unsigned addr) {
+    unsigned r;
+    asm volatile("ds_read_b32 %0, %1 offset:%2" : "=v"(r) : "v"(addr), "n"(OFF) : "memory");
+    return r;
+}
+
+__device__ __forceinline__ void lgkm_wait1(unsigned& a) {
+    asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(a)::"memory");
+}
+
+template <int OFF>
 __device__ __forceinline__ u32x2 lds_b64(unsigned addr) {
     u32x2 r;
     asm volatile("ds_read_b64 %0, %1 offset:%2" : "=v"(r) : "v"(addr), "n"(OFF) : "memory");
@@ -421,6 +433,8 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_bf16_kernel(AttnArgs a) 
     // KVMap words of a tile: 2 tile slots x 4 waves x 256 bytes; each wave
     // copies and reads only its own 256 bytes.
     __shared__ __attribute__((aligned(256))) unsigned char m_lds[2 * 4 * 256];
+    // Per-wave 2 KiB sink for copies whose data is not needed (KVMap kernel).
+    __shared__ __attribute__((aligned(1024))) unsigned char sink_lds[kMap ? 4 * 2048 : 16];
 
     const WgCoord c = decode_wg(a);
     if (!c.valid) return;  // whole workgroup: past the end of the layer order
@@ -498,13 +512,37 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_bf16_kernel(AttnArgs a) 
     unsigned mdec[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) mdec[i] = ~0u;
+    // Wave-uniform: some row of the wave's 16-row copy group maps into the
+    // arena. Almost every group holds none (an arena covers a few % of a
+    // frame's keys), and then neither the per-row decode nor the per-lane
+    // choice of source runs: the wave copies like the map-free kernel.
+    bool grp_mapped = false;
+    // Dword 2e+1 of a wave's map slot is the high word of its group's entry e
+    // (row 16*wave + e); an entry can name an arena row only when that word is
+    // 0. Each lane reads one dword of the slot of the next tile to decode
+    // (read_check) as soon as its map copy has landed, at the end of the
+    // iteration before, so the check below waits for nothing.
+    unsigned hw = ~0u;
+    auto read_check = [&](int t) {
+        if constexpr (!kMap) return;
+        hw = lds_b32<0>(m_wave + 1024u * (unsigned)(t & 1) + 4u * (unsigned)lane);
+    };
     auto decode_map = [&](int t) {
         if constexpr (!kMap) return;
-        wait_vm<0>();
-        const unsigned ad = m_wave + 1024u * (unsigned)(t & 1) + 8u * (unsigned)(lane >> 4);
-        u32x2 m0 = lds_b64<0>(ad), m1 = lds_b64<32>(ad), m2 = lds_b64<64>(ad), m3 = lds_b64<96>(ad);
+        const unsigned slot = m_wave + 1024u * (unsigned)(t & 1);
         const long left = kend - (kbeg + (long)t * kBf16BlockKeys);
         const int valid_rows = left < kBf16BlockKeys ? (int)left : kBf16BlockKeys;
+        // rows at or past the range end are zero-filled padding, not entries
+        lgkm_wait1(hw);
+        grp_mapped = __builtin_amdgcn_ballot_w64(lane < 32 && (lane & 1) && hw == 0u &&
+                                                 16 * wave + (lane >> 1) < valid_rows) != 0;
+        if (!grp_mapped) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) mdec[i] = ~0u;
+            return;
+        }
+        const unsigned ad = slot + 8u * (unsigned)(lane >> 4);
+        u32x2 m0 = lds_b64<0>(ad), m1 = lds_b64<32>(ad), m2 = lds_b64<64>(ad), m3 = lds_b64<96>(ad);
         lgkm_wait_tr(m0, m1, m2, m3);
         const u32x2 mw[4] = {m0, m1, m2, m3};
 #pragma unroll
@@ -560,6 +598,19 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_bf16_kernel(AttnArgs a) 
             __builtin_amdgcn_raw_ptr_buffer_load_lds(vrs, vd, 16, row_off + vofs, 0, 0,
                                                      kColdAux);
         }
+    };
+    // The copies interleaved with the QK MFMAs: the map-free kernel's copies
+    // (no per-lane source choice, no branch between the MFMAs). For a group
+    // with arena rows, whose copies were issued before the tile (copy_pair),
+    // they land in the wave's sink instead (scalar select of the LDS target).
+    const unsigned sink = (unsigned)(uintptr_t)sink_lds + 2048u * (unsigned)wave;
+    auto copy_plain = [&](int i) {
+        const bool to_sink = kMap && grp_mapped;
+        KVP_LDS void* kd = (KVP_LDS void*)(uintptr_t)(to_sink ? sink : koff + 1024u * i);
+        KVP_LDS void* vd = (KVP_LDS void*)(uintptr_t)(to_sink ? sink + 1024u : voff + 1024u * i);
+        const unsigned row_off = lane_row + 4u * i * rb;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(krs, kd, 16, row_off + kofs[i], 0, 0, kColdAux);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(vrs, vd, 16, row_off + vofs, 0, 0, kColdAux);
     };
 
     f32x16 o[4];
@@ -750,6 +801,8 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_bf16_kernel(AttnArgs a) 
 
     if (ntiles > 0) {
         load_map(0);
+        wait_vm<0>();
+        read_check(0);
         decode_map(0);
         if (ntiles > 1) load_map(1);
         prep_tile(0, k_lds0, v_lds0);
@@ -759,6 +812,7 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_bf16_kernel(AttnArgs a) 
     // Compiler-visible wait for every load so far (Q, map, tile 0): the loop
     // then never waits for vector memory on the Q registers' account.
     __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
+    if (ntiles > 1) read_check(1);
     for (int t = 0; t < ntiles; ++t) {
         // tile t lives in stage t & 1; tile t+1 streams into the other stage,
         // which every wave finished reading before the barrier that closed
@@ -780,17 +834,29 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_bf16_kernel(AttnArgs a) 
             decode_map(t + 1);
             if (kMap && t + 2 < ntiles) load_map(t + 2);
         } else if (kMap) {
+            grp_mapped = false;
 #pragma unroll
             for (int i = 0; i < 4; ++i) mdec[i] = ~0u;
         }
         prep_tile(t + 1, knext, vnext);
-        if (active) {
-            compute_tile(t, kcur, vcur, [&](int ks) {
-                if ((ks & 1) == 0) copy_pair(ks >> 1);
-            });
-        } else {
+        if (!active || (kMap && grp_mapped)) {
+            // inactive waves, and groups with arena rows (rare; wave-uniform):
+            // each row's source chosen per lane, copies issued before the
+            // tile's MFMAs
 #pragma unroll
             for (int i = 0; i < 4; ++i) copy_pair(i);
+        }
+        if (active) {
+            compute_tile(t, kcur, vcur, [&](int ks) {
+                if ((ks & 1) == 0) copy_plain(ks >> 1);
+            });
+        }
+        if (kMap && t + 2 < ntiles) {
+            // the map copy of tile t+2 was issued before this iteration's 8
+            // (or, for a group with arena rows, 16) tile copies: once at most
+            // 8 loads are outstanding it has landed
+            wait_vm<8>();
+            read_check(t + 2);
         }
         wg_barrier();
     }
@@ -1172,6 +1238,7 @@ LaunchPlan plan_launch(int dtype, int nq, int heads, int frames, long span, cons
     p.grid = base * p.splits;
     return p;
 }
+
 
 }  // namespace
 

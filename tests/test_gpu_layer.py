@@ -101,6 +101,55 @@ def test_layer_launch_matches_oracle_and_map_is_invisible(dtype, mode, window, T
     assert torch.equal(got, base)
 
 
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("api_kind", ["single_frame", "layer"])
+def test_kvmap_reads_the_arena_row_the_map_names(dtype, api_kind):
+    """Arena rows hold other data than the key rows they stand in for: the
+    output must be attention over K/V with every mapped row replaced by its
+    arena row (reference semantics, src/gated_attention_kernel.cu:73-85 and
+    :118-130), including rows in the last, partial key tile."""
+    frames, T, heads = 3, 1560, 2
+    D = heads * 128
+    q, k, v = _inputs(frames, T, heads, seed=29, dtype=dtype)
+    rng = np.random.default_rng(29)
+    region_rows = 200
+    full = frames * T
+    arena = torch.from_numpy(rng.standard_normal((frames * region_rows, 2 * D),
+                                                 dtype=np.float32))
+    if dtype == torch.bfloat16:
+        arena = at.round_bf16(arena)
+    kvmap = torch.full((frames * full,), -1, dtype=torch.int64)
+    want = torch.empty(frames * T, D)
+    for f in range(frames):
+        e = (f + 1) * T
+        # whole 16-row groups, single rows, and rows of the last partial tile
+        rows = set(rng.choice(e, size=120, replace=False).tolist())
+        rows |= set(range(e - 20, e)) | set(range(64, 80))
+        rows = sorted(rows)[:region_rows]
+        slots = rng.permutation(region_rows)[:len(rows)]
+        kf, vf = k[:e].clone(), v[:e].clone()
+        for r, sl in zip(rows, slots):
+            kvmap[f * full + r] = int(sl)
+            kf[r] = arena[f * region_rows + sl, :D]
+            vf[r] = arena[f * region_rows + sl, D:]
+        want[f * T:e] = at.attention_keys(q[f * T:e], kf, vf, heads)
+    qd, kd, vd = (x.to(DEV).to(dtype).contiguous() for x in (q, k, v))
+    ad, md = arena.to(DEV).to(dtype), kvmap.to(DEV)
+    if api_kind == "layer":
+        got = _layer(dtype, qd, kd, vd, frames, T, heads, "cross", 0, ad, md,
+                     region_rows * 2 * D * ad.element_size(), full)
+    else:
+        got = torch.empty_like(qd)
+        for f in range(frames):
+            sl = slice(f * T, (f + 1) * T)
+            fn = (api.attn_forward_single_frame if dtype == torch.float32
+                  else api.attn_forward_single_frame_bf16)
+            fn(qd[sl], kd, vd, ad[f * region_rows:], md[f * full:(f + 1) * full], got[sl], T,
+               D, heads, 1, f)
+        torch.cuda.synchronize()
+    _check(got.float().cpu(), want, dtype)
+
+
 def test_cold_rows_nt_is_a_cache_hint_only():
     """Non-temporal loads of original rows change no output bit."""
     frames, T, heads = 4, 1560, 2
