@@ -602,15 +602,22 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_bf16_kernel(AttnArgs a) 
     // The copies interleaved with the QK MFMAs: the map-free kernel's copies
     // (no per-lane source choice, no branch between the MFMAs). For a group
     // with arena rows, whose copies were issued before the tile (copy_pair),
-    // they land in the wave's sink instead (scalar select of the LDS target).
+    // they land in the wave's sink instead (scalar select of the LDS target
+    // and the descriptor).
     const unsigned sink = (unsigned)(uintptr_t)sink_lds + 2048u * (unsigned)wave;
+    // A sinked copy goes through a descriptor of zero records: it reads
+    // nothing from memory (out-of-range loads return zeros).
+    const __amdgpu_buffer_rsrc_t empty_rs =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<unsigned char*>(Kb), (short)0, 0, kBufFlags);
     auto copy_plain = [&](int i) {
         const bool to_sink = kMap && grp_mapped;
         KVP_LDS void* kd = (KVP_LDS void*)(uintptr_t)(to_sink ? sink : koff + 1024u * i);
         KVP_LDS void* vd = (KVP_LDS void*)(uintptr_t)(to_sink ? sink + 1024u : voff + 1024u * i);
+        const __amdgpu_buffer_rsrc_t ks = to_sink ? empty_rs : krs;
+        const __amdgpu_buffer_rsrc_t vs = to_sink ? empty_rs : vrs;
         const unsigned row_off = lane_row + 4u * i * rb;
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(krs, kd, 16, row_off + kofs[i], 0, 0, kColdAux);
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(vrs, vd, 16, row_off + vofs, 0, 0, kColdAux);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(ks, kd, 16, row_off + kofs[i], 0, 0, kColdAux);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(vs, vd, 16, row_off + vofs, 0, 0, kColdAux);
     };
 
     f32x16 o[4];
