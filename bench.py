@@ -50,6 +50,7 @@ sys.path.insert(0, str(ROOT / "cuda-kv-persistence_amd"))
 
 METRIC = "attn ms/frame + MFMA util + HBM read bytes/frame vs policy None, Wan2.1-1.3B"
 BF16_PEAK_TFLOPS = 2516.6  # MI355X dense bf16 MFMA
+FP32_PEAK_TFLOPS = 157.3   # MI355X fp32 MFMA
 HBM_PEAK_GBS = 8000.0
 
 
@@ -548,6 +549,60 @@ def measure_counters(args, cfg, headline):
     return res
 
 
+def fp32_legs(torch, stream, api, FramePipeline, workloads, reps=50):
+    """C1 and C2, the reference's own precision: one 1560-token frame, fp32,
+    12 x 128, intra-frame attention; C1 policy none, C2 the motion-gated
+    arena of 22 fp32 tiles. ms per frame (pipeline step: staging + attention)
+    and the attention kernel's TFLOP/s against the fp32 MFMA peak."""
+    out = {}
+    for name, policy in (("c1", "none"), ("c2", "motion")):
+        c = workloads.CONFIGS[name]
+        T, D, H = c.tokens, workloads.HIDDEN, workloads.HEADS
+        q, k, v = workloads.qkv_device(1, T, seed=42, dtype=torch.float32)
+        o = torch.empty_like(q)
+        pl = FramePipeline(policy, cross=False, streaming=False, frames=1, T=T, D=D, heads=H,
+                           tile_tokens=workloads.TILE_TOKENS, set_aside_bytes=c.set_aside,
+                           dtype=api.FP32)
+        pl.set_stream(stream)
+        pl.set_scores(workloads.motion_for(c) if policy != "none" else None)
+        for _ in range(5):
+            pl.run(q, k, v, o)
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            pl.run(q, k, v, o)
+        e1.record()
+        torch.cuda.synchronize()
+        ms = e0.elapsed_time(e1) / reps
+        # attention alone, the pipeline's own launch (arena region and map slice)
+        gated = policy != "none"
+        for rep in range(2):
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record()
+            for _ in range(reps):
+                api.attn_forward_frames(api.FP32, q, k, v, pl.layer_arena_ptr() if gated else None,
+                                        pl.layer_map_ptr() if gated else None, o, 1, T, D, H,
+                                        cross=False,
+                                        arena_frame_bytes=pl.layer_region_bytes() if gated else 0,
+                                        map_frame_stride=pl.layer_map_stride() if gated else 0,
+                                        stream=stream)
+            b.record()
+            torch.cuda.synchronize()
+        am = a.elapsed_time(b) / reps
+        tf = c.flops_per_layer() / (am * 1e-3) / 1e12
+        out[name] = {"workload": f"{name}: 1 frame x {T} tokens, 12 x 128, fp32, intra-frame, "
+                                 f"policy {policy}" + (", arena 22 fp32 tiles" if gated else ""),
+                     "pipeline_ms_per_frame": round(ms, 4),
+                     "attn_kernel_ms_per_frame": round(am, 4),
+                     "attn_tflops": round(tf, 2),
+                     "attn_mfma_frac": round(tf / FP32_PEAK_TFLOPS, 4),
+                     "peak": FP32_PEAK_TFLOPS}
+        pl.close()
+        log(f"leg {name}: {ms:.4f} ms/frame, attention {tf:.1f} TFLOP/s fp32")
+    return out
+
+
 def compulsory_read_bytes_per_frame(cfg):
     """Algorithmic read bytes of the layer launch per query frame: the launch
     reads every frame's Q rows once and, since every key row of the layer is
@@ -747,6 +802,7 @@ def main():
     # --- other multi-frame configurations (motion policy) --------------------------
     legs = {}
     if not args.no_legs:
+        legs.update(fp32_legs(torch, stream, api, FramePipeline, workloads))
         for name in ("c3", "c4", "c5"):
             if name == args.config:
                 continue

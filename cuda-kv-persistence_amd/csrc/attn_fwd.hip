@@ -1303,7 +1303,7 @@ int validate_launch(const AttnLaunch& L) {
         set_error("attention: negative frame stride");
         return 1;
     }
-    if (L.kend_step != 0 && !L.layer) {
+    if (L.kend_step != 0 && !L.layer && L.frames > 1) {
         set_error("attention: per-frame key ranges need a layer launch");
         return 1;
     }
@@ -1343,14 +1343,17 @@ int prepare_launch(const AttnLaunch& L, const DeviceInfo& di, AttnArgs& a, Launc
     if (span_last > max_span) span_last = max_span;
 
     const int bk = L.dtype == 1 ? kBf16BlockKeys : kF32BlockKeys;
-    if (L.layer) {
+    // A one-frame layer is an ordinary launch: it may then split its key
+    // range when its workgroups underfill the GPU.
+    const bool layer = L.layer && L.frames > 1;
+    if (layer) {
         p.nqb = (L.nq + kBlockQ - 1) / kBlockQ;
         p.splits = 1;
         p.keys_per_split = ((span_last + bk - 1) / bk) * bk;
         const long cols = (long)L.heads * p.nqb;
         p.grid = (long)kNumXcd * ((cols + kNumXcd - 1) / kNumXcd) * L.frames;
     } else {
-        p = plan_launch(L.dtype, L.nq, L.heads, L.frames, L.key_end - L.key_begin, di);
+        p = plan_launch(L.dtype, L.nq, L.heads, L.frames, span_last, di);
     }
     if (p.grid > 0x7fffffffL) {
         set_error("attention: grid too large");
@@ -1381,7 +1384,7 @@ int prepare_launch(const AttnLaunch& L, const DeviceInfo& di, AttnArgs& a, Launc
     a.frames = L.frames;
     a.splits = p.splits;
     a.nqb = p.nqb;
-    a.layer_order = L.layer ? 1 : 0;
+    a.layer_order = layer ? 1 : 0;
     a.scale_log2 = kLog2e / sqrtf((float)kHeadDim);
     return 0;
 }
