@@ -584,7 +584,6 @@ def fp32_legs(torch, stream, api, FramePipeline, workloads, reps=50):
                 api.attn_forward_frames(api.FP32, q, k, v, pl.layer_arena_ptr() if gated else None,
                                         pl.layer_map_ptr() if gated else None, o, 1, T, D, H,
                                         cross=False,
-                                        arena_frame_bytes=pl.layer_region_bytes() if gated else 0,
                                         map_frame_stride=pl.layer_map_stride() if gated else 0,
                                         stream=stream)
             b.record()
@@ -707,7 +706,6 @@ def main():
         T, D, H, F = c.tokens, workloads.HIDDEN, workloads.HEADS, c.frames
         arena = pl.layer_arena_ptr() if gated else None
         kvmap = pl.layer_map_ptr() if gated else None
-        rb = pl.layer_region_bytes() if gated else 0
         ms = pl.layer_map_stride() if gated else 0
         evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
                for _ in data]
@@ -717,7 +715,7 @@ def main():
                 a.record()
                 api.attn_forward_frames(api.BF16, q, k, v, arena, kvmap, scratch, F, T, D, H,
                                         cross=True, window_frames=c.window,
-                                        arena_frame_bytes=rb, map_frame_stride=ms,
+                                        map_frame_stride=ms,
                                         cold_rows_nt=args.cold_rows_nt and gated,
                                         stream=stream)
                 b.record()

@@ -103,6 +103,54 @@ __global__ __launch_bounds__(stage::kRunThreads) void stage_runs_kernel(const Ru
     stage::stage_runs_block(a, (int)blockIdx.x);
 }
 
+// Layer staging: workgroups [0, n_copies) copy one run each, the ones after
+// that write one KVMap run each. A copy run moves n arena rows of
+// 2 * cpr 16-byte chunks; chunk w < cpr of a row comes from its K row, the
+// rest from its V row. Each thread keeps four chunks in flight before it
+// stores them.
+constexpr int kLayerThreads = 256;
+constexpr int kLayerBatch = 4;
+
+__global__ __launch_bounds__(kLayerThreads) void layer_stage_kernel(
+    const LayerCopyRun* __restrict__ copies, long n_copies,
+    const LayerMapRun* __restrict__ map_runs, unsigned char* __restrict__ arena,
+    const unsigned char* __restrict__ k, const unsigned char* __restrict__ v, unsigned cpr,
+    long* __restrict__ map) {
+    typedef __attribute__((ext_vector_type(4))) unsigned int u32x4;
+    const long b = blockIdx.x;
+    if (b < n_copies) {
+        const LayerCopyRun r = copies[b];
+        const unsigned per_row = 2u * cpr;
+        const unsigned total = (unsigned)r.n * per_row;
+        const long rb = 16L * cpr;
+        for (unsigned c0 = 0; c0 < total; c0 += kLayerBatch * kLayerThreads) {
+            u32x4 val[kLayerBatch];
+            unsigned char* dst[kLayerBatch];
+#pragma unroll
+            for (int u = 0; u < kLayerBatch; ++u) {
+                const unsigned c = c0 + u * kLayerThreads + threadIdx.x;
+                dst[u] = nullptr;
+                if (c < total) {
+                    const unsigned row = c / per_row;
+                    const unsigned w = c - row * per_row;
+                    const long src_row = (long)r.src_row + row;
+                    const unsigned char* src = w < cpr ? k + src_row * rb + 16L * w
+                                                       : v + src_row * rb + 16L * (w - cpr);
+                    val[u] = *reinterpret_cast<const u32x4*>(src);
+                    dst[u] = arena + ((long)r.dst_row + row) * 2 * rb + 16L * w;
+                }
+            }
+#pragma unroll
+            for (int u = 0; u < kLayerBatch; ++u)
+                if (dst[u]) *reinterpret_cast<u32x4*>(dst[u]) = val[u];
+        }
+    } else {
+        const LayerMapRun m = map_runs[b - n_copies];
+        for (int j = (int)threadIdx.x; j < m.n; j += kLayerThreads)
+            map[m.index + j] = m.value < 0 ? -1L : (long)m.value + j;
+    }
+}
+
 struct Stager {
     unsigned char* host = nullptr;  // mapped pinned memory
     unsigned char* dev = nullptr;   // device view of `host`
@@ -413,5 +461,59 @@ int stage_plan_launch(const void* plan, void* stream) {
 }
 
 void stage_plan_free(void* plan) { delete static_cast<StagePlan*>(plan); }
+
+int layer_stage_launch(void* stager, void* arena, const void* k, const void* v, long row_bytes,
+                       const LayerCopyRun* copies, long n_copies, long* map,
+                       const LayerMapRun* map_runs, long n_map_runs, void* stream) {
+    Stager* st = static_cast<Stager*>(stager);
+    if (!st) {
+        set_error("layer stage: null stager");
+        return 1;
+    }
+    if (n_copies < 0 || n_map_runs < 0 || n_copies + n_map_runs > INT_MAX) {
+        set_error("layer stage: bad run counts");
+        return 1;
+    }
+    if (n_copies + n_map_runs == 0) return 0;
+    if (n_copies > 0 && (!arena || !k || !v || row_bytes <= 0 || row_bytes % 16 ||
+                         ((uintptr_t)arena | (uintptr_t)k | (uintptr_t)v) % 16)) {
+        set_error("layer stage: copies need 16-byte aligned arena, K, V and row size");
+        return 1;
+    }
+    if (n_map_runs > 0 && !map) {
+        set_error("layer stage: map runs without a map");
+        return 1;
+    }
+    const size_t copy_bytes = align256((size_t)n_copies * sizeof(LayerCopyRun));
+    const size_t need = copy_bytes + align256((size_t)n_map_runs * sizeof(LayerMapRun));
+    if (!st->reserve(need)) {
+        set_error("layer stage: descriptor ring allocation failed");
+        return 1;
+    }
+    unsigned char* h = st->host + st->head;
+    unsigned char* d = st->dev + st->head;
+    if (n_copies > 0) memcpy(h, copies, (size_t)n_copies * sizeof(LayerCopyRun));
+    if (n_map_runs > 0) memcpy(h + copy_bytes, map_runs, (size_t)n_map_runs * sizeof(LayerMapRun));
+    hipStream_t hs = static_cast<hipStream_t>(stream);
+    hipLaunchKernelGGL(layer_stage_kernel, dim3((unsigned)(n_copies + n_map_runs)),
+                       dim3(kLayerThreads), 0, hs, reinterpret_cast<const LayerCopyRun*>(d),
+                       n_copies, reinterpret_cast<const LayerMapRun*>(d + copy_bytes),
+                       static_cast<unsigned char*>(arena), static_cast<const unsigned char*>(k),
+                       static_cast<const unsigned char*>(v), (unsigned)(row_bytes / 16), map);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) {
+        set_error("layer stage launch: %s", hipGetErrorString(e));
+        return 1;
+    }
+    hipEvent_t ev = st->take_event();
+    if (!ev || hipEventRecord(ev, hs) != hipSuccess) {
+        if (ev) st->spare.push_back(ev);
+        (void)hipStreamSynchronize(hs);
+    } else {
+        st->inflight.push_back(ev);
+    }
+    st->head += need;
+    return 0;
+}
 
 }  // namespace kvp

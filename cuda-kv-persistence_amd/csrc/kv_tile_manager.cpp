@@ -8,6 +8,7 @@
 #include "kv_tile_manager.h"
 #include "kvp_internal.h"
 
+#include <algorithm>
 #include <cstdint>
 #include <cstdio>
 
@@ -204,6 +205,64 @@ bool KVTileManager::arena_stage(const void* k_dev, size_t k_bytes,
     return true;
 }
 
+long KVTileManager::arena_stage_rows(const char* k_first, size_t k_bytes, const char* v_first,
+                                     size_t v_bytes, long n, long* out_slots) {
+    const size_t total = k_bytes + v_bytes;
+    const size_t stride = arena_row_stride_floats_ * sizeof(float);
+    if (!plan_only_ || total == 0 || stride == 0 || n <= 0) {
+        long m = 0;
+        for (; m < n; ++m) {
+            long row = -1;
+            if (!arena_stage(k_first ? k_first + m * (long)k_bytes : nullptr, k_bytes,
+                             v_first ? v_first + m * (long)v_bytes : nullptr, v_bytes, &row))
+                break;
+            if (out_slots) out_slots[m] = row;
+        }
+        return m;
+    }
+    // Plan-only: nothing to record, and each gate of arena_stage holds for
+    // a prefix of the rows, so the staged count is the smallest prefix bound.
+    auto fit = [&](size_t limit) -> size_t {
+        return limit >= arena_used_ ? (limit - arena_used_) / total : 0;
+    };
+    size_t m = std::min(fit(budget_bytes_), fit(arena_cap_));
+    const size_t last_row = arena_cap_ >= total ? (arena_cap_ - total) / stride : 0;
+    const size_t by_row = (arena_cap_ >= total && last_row + 1 > arena_next_row_)
+                              ? last_row + 1 - arena_next_row_ : 0;
+    m = std::min(std::min(m, by_row), (size_t)n);
+    if (out_slots)
+        for (size_t i = 0; i < m; ++i) out_slots[i] = (long)(arena_next_row_ + i);
+    arena_next_row_ += m;
+    arena_used_ += m * total;
+    return (long)m;
+}
+
+long KVTileManager::streaming_stage_rows(long row_first, const char* k_first, size_t k_bytes,
+                                         const char* v_first, size_t v_bytes, long n,
+                                         long* out_slots, long* copied) {
+    long m = 0, c = 0;
+    for (; m < n; ++m) {
+        const long row = row_first + m;
+        if (row == KvtmRowTable::kEmpty || row == KvtmRowTable::kTomb) break;
+        // sticky hit (changed = false): the slot, no copy, no state change
+        const long held = row_slot_.find(row);
+        if (held >= 0) {
+            if (out_slots) out_slots[m] = held;
+            continue;
+        }
+        long slot = -1;
+        bool restaged = false;
+        if (!streaming_stage(row, k_first ? k_first + m * (long)k_bytes : nullptr,
+                             k_bytes, v_first ? v_first + m * (long)v_bytes : nullptr, v_bytes,
+                             false, &slot, &restaged))
+            break;
+        if (restaged) ++c;
+        if (out_slots) out_slots[m] = slot;
+    }
+    if (copied) *copied = c;
+    return m;
+}
+
 bool KVTileManager::arena_apply_window() {
     const bool ok = flush();
     if (!initialized_ || arena_used_ == 0 || arena_used_ > max_window_bytes_)
@@ -233,6 +292,7 @@ bool KVTileManager::streaming_begin() {
     if (!arena_ && !plan_only_) return false;
     flush();
     row_slot_.clear();
+    row_slot_.reserve((size_t)std::max<long>(0, streaming_capacity_rows()));
     free_slots_.clear();
     // Highest slot pushed first so the first pop hands out slot 0.
     for (long s = streaming_capacity_rows() - 1; s >= 0; --s) free_slots_.push_back(s);
@@ -245,15 +305,16 @@ bool KVTileManager::streaming_stage(long row_id, const void* k_dev,
                                     size_t k_bytes, const void* v_dev,
                                     size_t v_bytes, bool changed,
                                     long* out_slot, bool* restaged) {
-    auto it = row_slot_.find(row_id);
-    if (it != row_slot_.end()) {
-        *out_slot = it->second;
+    if (row_id == KvtmRowTable::kEmpty || row_id == KvtmRowTable::kTomb) return false;
+    const long held = row_slot_.find(row_id);
+    if (held >= 0) {
+        *out_slot = held;
         if (!changed) {
             *restaged = false;  // sticky hit: slot content still valid
             return true;
         }
-        if (!row_fits(it->second, k_bytes + v_bytes)) return false;
-        if (!record_copy(it->second, k_dev, k_bytes, v_dev, v_bytes)) return false;
+        if (!row_fits(held, k_bytes + v_bytes)) return false;
+        if (!record_copy(held, k_dev, k_bytes, v_dev, v_bytes)) return false;
         staged_bytes_ += k_bytes + v_bytes;
         *restaged = true;
         return true;
@@ -263,7 +324,7 @@ bool KVTileManager::streaming_stage(long row_id, const void* k_dev,
     if (!row_fits(slot, k_bytes + v_bytes)) return false;
     if (!record_copy(slot, k_dev, k_bytes, v_dev, v_bytes)) return false;
     free_slots_.pop_back();
-    row_slot_[row_id] = slot;
+    row_slot_.insert(row_id, slot);
     staged_bytes_ += k_bytes + v_bytes;
     if (slot > slot_high_water_) slot_high_water_ = slot;
     *out_slot = slot;
@@ -272,10 +333,9 @@ bool KVTileManager::streaming_stage(long row_id, const void* k_dev,
 }
 
 bool KVTileManager::streaming_release(long row_id) {
-    auto it = row_slot_.find(row_id);
-    if (it == row_slot_.end()) return false;
-    free_slots_.push_back(it->second);
-    row_slot_.erase(it);
+    const long slot = row_slot_.erase(row_id);
+    if (slot < 0) return false;
+    free_slots_.push_back(slot);
     return true;
 }
 

@@ -73,6 +73,30 @@ void* stage_plan_create(void* stager, void* arena, long row_stride_bytes,
 int stage_plan_launch(const void* plan, void* stream);
 void stage_plan_free(void* plan);
 
+// Layer staging (kv_stage.hip): one launch that copies runs of consecutive
+// K/V rows into consecutive arena rows ([K row | V row] per arena row) and
+// writes runs of KVMap entries. Run tables travel through the stager's
+// mapped descriptor ring.
+constexpr int kLayerCopyRows = 32;     // rows per copy run (one workgroup)
+constexpr int kLayerMapEntries = 1024; // entries per map run (one workgroup)
+struct LayerCopyRun {
+    int src_row;  // first K/V row (index into k and v, row_bytes apart)
+    int dst_row;  // first arena row
+    int n;        // rows, 1..kLayerCopyRows
+    int pad;
+};
+struct LayerMapRun {
+    long index;   // first KVMap entry
+    int value;    // -1: n entries reset to -1; else entry j = value + j
+    int n;        // entries, 1..kLayerMapEntries
+};
+// The caller has checked every run against its buffers: src rows below
+// the K/V row count, dst rows below the arena's, map entries below the map's.
+// row_bytes: bytes of one K (or V) row, a multiple of 16.
+int layer_stage_launch(void* stager, void* arena, const void* k, const void* v, long row_bytes,
+                       const LayerCopyRun* copies, long n_copies, long* map,
+                       const LayerMapRun* map_runs, long n_map_runs, void* stream);
+
 // Grouped bf16 projection GEMM (proj_gemm.hip): for g < groups (1..3),
 // outs[g][r, n] = sum_k x[r, k] w[g*Ng + n, k] + bias[g*Ng + n]
 // (+ outs[g][r, n] when accumulate; fp32 output only). x, w bf16; bias fp32

@@ -21,13 +21,17 @@
 //     (prefix reset to -1, then the staged rows).
 //   * kvp_pipeline_run: a whole layer in two launches. Steps 1-3 run on the
 //     host for every frame first (a bookkeeping-only manager takes the same
-//     decisions); frame f's arena state goes to its own region of a layer
-//     arena (every mapped row copied to region f at its slot) and frame f's
-//     KVMap to its own slice of a layer map, all in one staging launch; then
-//     one attention launch covers every frame, each reading its own region
-//     and slice. Region f holds, at every slot frame f's map points to, what
-//     the single arena holds at frame f, so the outputs are those of
-//     frame-by-frame stepping, bit for bit.
+//     decisions: which rows each frame maps); then one staging launch and one
+//     attention launch cover every frame. K and V are fixed for the whole
+//     layer, so a row holds the same bytes in every frame that maps it: the
+//     layer arena holds each row mapped by any frame once (physical rows in
+//     first-mapped order), and frame f's slice of the layer map points each
+//     of its mapped rows at that row's physical row. The staging launch
+//     copies each such row once, as runs of consecutive rows, and writes the
+//     map entries that differ from the previous run, as runs. Every frame
+//     maps exactly the rows the single arena maps at that frame, holding the
+//     same bytes, so the outputs are those of frame-by-frame stepping, bit for
+//     bit; only the arena placement differs (physical rows, not slots).
 // Nothing synchronises the host per frame; all device work is ordered on the
 // pipeline's stream.
 
@@ -76,16 +80,38 @@ struct Pipeline {
 
     // layer mode (kvp_pipeline_run)
     std::unique_ptr<KVTileManager> layer_mgr;  // bookkeeping only
-    char* layer_arena = nullptr;               // frames regions of region_bytes
-    long region_rows = 0, region_bytes = 0;
+    char* layer_arena = nullptr;               // layer_cap physical rows
+    long region_rows = 0;                      // rows one frame may map
+    long layer_cap = 0;                        // physical rows of the layer arena
     long* layer_map = nullptr;                 // frames slices of map_stride entries
     long map_stride = 0;
-    std::vector<long> layer_mirror;            // device content of layer_map
-    std::vector<std::vector<long>> layer_rows; // per frame: rows mapped on the device
-    std::vector<int> layer_stamp;
-    int layer_step = 0;
-    std::vector<KvpRowCopy> layer_copies;
+    long seg_space = 0;                        // tiles one map slice can hold
+    // A frame's mapped rows, a tile at a time: rows [0, n) of tile gsrc
+    // (frame-major tile id over all frames), at map slice index idx.
+    struct Seg {
+        long idx;
+        long gsrc;
+        int n;
+    };
+    std::vector<Seg> segs;                     // the frame being planned
+    std::vector<std::vector<int>> seg_n;       // per frame: rows mapped per tile on the device
+    std::vector<std::vector<long>> seg_phys;   // per frame: their first physical row
+    std::vector<std::vector<long>> seg_list;   // per frame: tiles with seg_n > 0
+    std::vector<int> seg_mark;                 // tile idx -> frame plan that maps it
+    int seg_gen = 0;
+    std::vector<long> tile_phys;               // gsrc -> first physical row this run
+    std::vector<int> tile_gen;                 // run that set tile_phys
+    int layer_gen = 0;
+    long layer_nphys = 0;                      // physical rows assigned this run
+    std::vector<long> tile_slots;              // slots of one tile (host map)
+    std::vector<kvp::LayerCopyRun> layer_copies;
+    std::vector<kvp::LayerMapRun> layer_updates;
     void* layer_stager = nullptr;
+    KVTileManager* last_mgr = nullptr;         // manager of the last step or run
+    // plan-only layer runs: the staging launch applied on the host
+    std::vector<long> plan_map;                // the layer map
+    std::vector<long> plan_src;                // physical row -> K/V row
+    std::vector<int> plan_stamp;               // run that wrote a map entry
 
     ~Pipeline() {
         mgr.reset();
@@ -104,14 +130,10 @@ long window_first_frame(const Pipeline& p, int f) {
     return (p.cross && p.window > 0 && f + 1 > p.window) ? f + 1 - p.window : 0;
 }
 
-// Steps 1-3 of a gated frame on manager `mgr`: selection, streaming release
-// and staging, leaving the frame's mapped rows in p.map_rows / p.map_slots
-// and its host map in p.h_map. Host bookkeeping only (a manager with a device
-// arena records its copies for the next flush).
-int plan_frame_host(Pipeline& p, KVTileManager& mgr, int f, const char* k, const char* v,
-                    const float* scores_flat) {
+// Steps 1-2 of a gated frame on manager `mgr`: selection (ids in p.ids,
+// p.count of them) and the streaming release of tiles that dropped out.
+int select_and_release(Pipeline& p, KVTileManager& mgr, int f, const float* scores_flat) {
     const long T = p.T;
-    const long row_bytes = (long)p.D * p.elem;
     if (!scores_flat) {
         kvp::set_error("pipeline: policy %s needs motion scores", p.policy->name());
         return 1;
@@ -157,6 +179,18 @@ int plan_frame_host(Pipeline& p, KVTileManager& mgr, int f, const char* k, const
             for (long r = 0; r < c; ++r) mgr.streaming_release(src_f * T + t0 + r);
         }
     }
+    return 0;
+}
+
+// Steps 1-3 of a gated frame on manager `mgr`: selection, streaming release
+// and staging, leaving the frame's mapped rows in p.map_rows / p.map_slots
+// and its host map in p.h_map. Host bookkeeping only (a manager with a device
+// arena records its copies for the next flush).
+int plan_frame_host(Pipeline& p, KVTileManager& mgr, int f, const char* k, const char* v,
+                    const float* scores_flat) {
+    const long T = p.T;
+    const long row_bytes = (long)p.D * p.elem;
+    if (select_and_release(p, mgr, f, scores_flat)) return 1;
 
     // 3. staging + host map
     mgr.arena_begin_step();
@@ -208,6 +242,7 @@ int plan_frame(Pipeline& p, int f, const char* k, const char* v, const float* sc
                void** plan) {
     *plan = nullptr;
     KVTileManager& mgr = *p.mgr;
+    p.last_mgr = &mgr;
     if (plan_frame_host(p, mgr, f, k, v, scores_flat)) return 1;
 
     // 4. row copies + changed map entries, as one staging plan
@@ -318,7 +353,9 @@ int step_frame(Pipeline& p, int f, const char* q, const char* k, const char* v, 
     return 0;
 }
 
-// Layer-mode device state, created at the first kvp_pipeline_run.
+// Layer-mode state, created at the first kvp_pipeline_run: the bookkeeping
+// manager and tile tables, and (unless plan-only) the device arena, map and
+// stager.
 int layer_setup(Pipeline& p) {
     if (p.layer_mgr) return 0;
     const long row_bytes = (long)p.D * p.elem;
@@ -330,63 +367,173 @@ int layer_setup(Pipeline& p) {
         kvp::set_error("pipeline: layer manager init failed");
         return 1;
     }
+    // A frame maps at most region_rows rows (the budget / slot capacity);
+    // physical rows are handed out a whole tile at a time, so one frame
+    // usually adds at most region_rows + tile_tokens of them. The arena grows
+    // in the rare layer that needs more (never past frames * T rows).
     p.region_rows = p.set_aside / (2 * row_bytes);
-    p.region_bytes = p.region_rows * 2 * row_bytes;
+    p.layer_cap = std::min((long)p.frames * (p.region_rows + p.tile_tokens), (long)p.frames * p.T);
     p.map_stride = p.cross ? (long)p.frames * p.T : (long)p.T;
+    p.seg_space = p.cross ? (long)p.frames * p.num_tiles : p.num_tiles;
     const long map_entries = (long)p.frames * p.map_stride;
+    p.seg_n.assign((size_t)p.frames, std::vector<int>((size_t)p.seg_space, 0));
+    p.seg_phys.assign((size_t)p.frames, std::vector<long>((size_t)p.seg_space, -1L));
+    p.seg_list.assign((size_t)p.frames, {});
+    p.seg_mark.assign((size_t)p.seg_space, 0);
+    p.tile_phys.assign((size_t)p.frames * p.num_tiles, -1L);
+    p.tile_gen.assign((size_t)p.frames * p.num_tiles, 0);
+    p.tile_slots.assign((size_t)p.tile_tokens, -1L);
+    if (p.plan_only) {
+        p.plan_map.assign((size_t)map_entries, -1L);
+        p.plan_stamp.assign((size_t)map_entries, 0);
+        return 0;
+    }
     p.layer_arena = static_cast<char*>(
-        kvp_dev_alloc((size_t)std::max<long>(1, p.frames * p.region_bytes)));
+        kvp_dev_alloc((size_t)std::max<long>(1, p.layer_cap * 2 * row_bytes)));
     p.layer_map = static_cast<long*>(kvp_dev_alloc((size_t)map_entries * sizeof(long)));
     p.layer_stager = kvp_stager_create();
     if (!p.layer_arena || !p.layer_map || !p.layer_stager) {
         kvp::set_error("pipeline: layer arena / map allocation failed");
         return 1;
     }
-    p.layer_mirror.assign((size_t)map_entries, -1L);
-    p.layer_rows.assign((size_t)p.frames, {});
-    p.layer_stamp.assign((size_t)p.map_stride, 0);
-    // the device map starts as all -1, matching the mirror
+    // the device map starts as all -1, matching seg_n
     if (kvp_stage_run(p.layer_stager, nullptr, 0, nullptr, 0, p.layer_map, map_entries, nullptr,
                       nullptr, 0, p.stream))
         return 1;
     return 0;
 }
 
-// Frame f's share of the layer staging launch: every mapped row copied into
-// region f at its slot, and the entries of map slice f that change.
-void layer_collect(Pipeline& p, int f, const char* k, const char* v) {
+// Step 3 of a gated frame in layer mode, a tile at a time: the manager
+// takes the decisions of plan_frame_host's row loop (batched per tile, same
+// order, same stop at a tile's first refused row), and the frame's mapped
+// rows are kept as segments in p.segs. The host map is written for the last
+// frame of the layer only (introspection of the last step).
+void plan_frame_layer(Pipeline& p, KVTileManager& mgr, int f, const char* k, const char* v) {
+    const long T = p.T;
     const long row_bytes = (long)p.D * p.elem;
+    const bool last = f + 1 == p.frames;
+    mgr.arena_begin_step();
+    if (last) std::fill(p.h_map.begin(), p.h_map.begin() + (size_t)(f + 1) * T, -1L);
+    p.segs.clear();
+    p.staged_tiles = 0;
+    p.copy_rows = 0;
+    for (int i = 0; i < p.count; ++i) {
+        const long gid = p.ids[i];
+        const long src_f = p.cross ? gid / p.num_tiles : f;
+        const long tile = p.cross ? gid % p.num_tiles : gid;
+        // uniform hands out ids 0..slots-1 whatever the candidate count; an
+        // id past the last frame names rows outside K/V and stages nothing
+        if (src_f >= p.frames) continue;
+        const long t0 = tile * p.tile_tokens;
+        const long c = std::min((long)p.tile_tokens, T - t0);
+        const long row0 = src_f * T + t0;
+        const char* kp = k ? k + row0 * row_bytes : nullptr;
+        const char* vp = v ? v + row0 * row_bytes : nullptr;
+        long* slots = last ? p.tile_slots.data() : nullptr;
+        long n, copied = 0;
+        if (p.streaming) {
+            n = mgr.streaming_stage_rows(row0, kp, (size_t)row_bytes, vp, (size_t)row_bytes, c,
+                                         slots, &copied);
+        } else {
+            n = mgr.arena_stage_rows(kp, (size_t)row_bytes, vp, (size_t)row_bytes, c, slots);
+            copied = n;
+        }
+        p.copy_rows += copied;
+        if (last)
+            for (long j = 0; j < n; ++j) p.h_map[(size_t)(row0 + j)] = p.tile_slots[(size_t)j];
+        if (n == c) ++p.staged_tiles;
+        if (n > 0)
+            p.segs.push_back(Pipeline::Seg{p.cross ? src_f * p.num_tiles + tile : tile,
+                                           src_f * p.num_tiles + tile, (int)n});
+    }
+}
+
+// Copy of c K/V rows from row `row` to physical rows [phys, phys + c),
+// appended to the run table in runs of at most ~24 KiB.
+void layer_add_copy(Pipeline& p, long row, long phys, long c) {
+    const long row_bytes = 2L * p.D * p.elem;
+    const long per_run = std::max<long>(1, std::min<long>(kvp::kLayerCopyRows, 24576 / row_bytes));
+    for (long j = 0; j < c; j += per_run)
+        p.layer_copies.push_back(kvp::LayerCopyRun{(int)(row + j), (int)(phys + j),
+                                                   (int)std::min(per_run, c - j), 0});
+}
+
+// Map entries [index, index + n) set to value + j (value -1: reset).
+void layer_add_update(Pipeline& p, long index, long value, long n) {
+    for (long j = 0; j < n; j += kvp::kLayerMapEntries)
+        p.layer_updates.push_back(kvp::LayerMapRun{
+            index + j, value < 0 ? -1 : (int)(value + j),
+            (int)std::min<long>(kvp::kLayerMapEntries, n - j)});
+}
+
+// Frame f's share of the layer staging launch: physical rows (and their
+// copy) for every tile the frame maps that has none yet this run, a whole
+// tile each, and the runs of map slice f that differ from what the device
+// holds. Write runs cover the rows a tile maps now; reset runs only rows
+// no tile of the frame maps now, so the runs of one launch never overlap.
+int layer_collect(Pipeline& p, int f) {
+    const long T = p.T;
     const long base = (long)f * p.map_stride;
-    const long rel = p.cross ? 0 : (long)f * p.T;  // intra slices are frame-relative
-    ++p.layer_step;
-    for (size_t i = 0; i < p.map_rows.size(); ++i) {
-        const long r = p.map_rows[i];
-        const long slot = p.map_slots[i];
-        KvpRowCopy c;
-        c.k_src = k + r * row_bytes;
-        c.v_src = v + r * row_bytes;
-        c.dst_row = (long)f * p.region_rows + slot;
-        c.k_bytes = (unsigned)row_bytes;
-        c.v_bytes = (unsigned)row_bytes;
-        p.layer_copies.push_back(c);
-        const long e = r - rel;
-        p.layer_stamp[(size_t)e] = p.layer_step;
-        if (p.layer_mirror[(size_t)(base + e)] != slot) {
-            p.upd_rows.push_back(base + e);
-            p.upd_vals.push_back(slot);
-            p.layer_mirror[(size_t)(base + e)] = slot;
+    const long rel = p.cross ? 0 : (long)f * T;  // intra slices are frame-relative
+    std::vector<int>& sn = p.seg_n[(size_t)f];
+    std::vector<long>& sp = p.seg_phys[(size_t)f];
+    std::vector<long>& list = p.seg_list[(size_t)f];
+    ++p.seg_gen;
+    for (const Pipeline::Seg& s : p.segs) {
+        const long tile = s.gsrc % p.num_tiles;
+        const long row0 = (s.gsrc / p.num_tiles) * T + tile * p.tile_tokens;
+        if (p.tile_gen[(size_t)s.gsrc] != p.layer_gen) {
+            const long c = std::min((long)p.tile_tokens, T - tile * p.tile_tokens);
+            if (p.layer_nphys + c > 0x7fffffffL || row0 + c > 0x7fffffffL) {
+                kvp::set_error("pipeline: layer arena rows exceed int");
+                return 1;
+            }
+            p.tile_gen[(size_t)s.gsrc] = p.layer_gen;
+            p.tile_phys[(size_t)s.gsrc] = p.layer_nphys;
+            layer_add_copy(p, row0, p.layer_nphys, c);
+            p.layer_nphys += c;
         }
+        const long ph = p.tile_phys[(size_t)s.gsrc];
+        const long e0 = base + row0 - rel;
+        const int old_n = sn[(size_t)s.idx];
+        if (old_n != s.n || sp[(size_t)s.idx] != ph) layer_add_update(p, e0, ph, s.n);
+        if (old_n > s.n) layer_add_update(p, e0 + s.n, -1, old_n - s.n);
+        p.seg_mark[(size_t)s.idx] = p.seg_gen;
     }
-    std::vector<long>& prev = p.layer_rows[(size_t)f];
-    for (long e : prev) {
-        if (p.layer_stamp[(size_t)e] != p.layer_step && p.layer_mirror[(size_t)(base + e)] != -1) {
-            p.upd_rows.push_back(base + e);
-            p.upd_vals.push_back(-1);
-            p.layer_mirror[(size_t)(base + e)] = -1;
-        }
+    for (long idx : list) {
+        if (p.seg_mark[(size_t)idx] == p.seg_gen) continue;
+        const long gsrc = p.cross ? idx : (long)f * p.num_tiles + idx;
+        const long row0 = (gsrc / p.num_tiles) * T + (gsrc % p.num_tiles) * p.tile_tokens;
+        layer_add_update(p, base + row0 - rel, -1, sn[(size_t)idx]);
+        sn[(size_t)idx] = 0;
+        sp[(size_t)idx] = -1;
     }
-    prev.clear();
-    for (long r : p.map_rows) prev.push_back(r - rel);
+    list.clear();
+    for (const Pipeline::Seg& s : p.segs) {
+        sn[(size_t)s.idx] = s.n;
+        sp[(size_t)s.idx] = p.tile_phys[(size_t)s.gsrc];
+        list.push_back(s.idx);
+    }
+    return 0;
+}
+
+// Grow the layer arena to hold the run's physical rows (rare: a layer with
+// many partly mapped tiles). The old arena may still be read by earlier
+// launches on the stream, so the stream is drained first.
+int layer_reserve(Pipeline& p) {
+    if (p.layer_nphys <= p.layer_cap) return 0;
+    const long row_bytes = (long)p.D * p.elem;
+    const long cap = std::min(std::max(p.layer_nphys, 2 * p.layer_cap), (long)p.frames * p.T);
+    if (kvp_stream_sync(p.stream)) return 1;
+    kvp_dev_free(p.layer_arena);
+    p.layer_arena = static_cast<char*>(kvp_dev_alloc((size_t)cap * 2 * row_bytes));
+    if (!p.layer_arena) {
+        p.layer_cap = 0;
+        kvp::set_error("pipeline: layer arena growth to %ld rows failed", cap);
+        return 1;
+    }
+    p.layer_cap = cap;
+    return 0;
 }
 
 // One attention launch over all frames of the layer.
@@ -398,10 +545,9 @@ int layer_attention(Pipeline& p, const char* q, const char* k, const char* v, ch
     L.v = v;
     L.out = out;
     if (p.persist) {
-        L.arena = p.layer_arena;
+        L.arena = p.layer_arena;  // one arena for every frame
         L.kvmap = p.layer_map;
         L.map_fstride = p.map_stride;
-        L.arena_fstride = p.region_bytes;
     }
     L.nq = p.T;
     L.D = p.D;
@@ -426,38 +572,68 @@ int layer_attention(Pipeline& p, const char* q, const char* k, const char* v, ch
 
 // A whole layer: host plans of every frame, one staging launch for all
 // frames' arena regions and map slices, one attention launch.
+// The staging launch of a plan-only layer run, applied on the host: the
+// layer map and the physical rows' sources. Fails when two runs of the
+// launch would write one physical row or one map entry (the workgroups of
+// one launch run in no fixed order).
+int layer_apply_host(Pipeline& p) {
+    p.plan_src.assign((size_t)p.layer_nphys, -1L);
+    for (const kvp::LayerCopyRun& r : p.layer_copies) {
+        for (int j = 0; j < r.n; ++j) {
+            const long d = (long)r.dst_row + j;
+            if (d < 0 || d >= p.layer_nphys || p.plan_src[(size_t)d] >= 0) {
+                kvp::set_error("pipeline: copy runs overlap or leave the arena at row %ld", d);
+                return 1;
+            }
+            p.plan_src[(size_t)d] = (long)r.src_row + j;
+        }
+    }
+    const int gen = p.layer_gen;
+    for (const kvp::LayerMapRun& m : p.layer_updates) {
+        for (int j = 0; j < m.n; ++j) {
+            const long e = m.index + j;
+            if (e < 0 || e >= (long)p.plan_map.size() || p.plan_stamp[(size_t)e] == gen) {
+                kvp::set_error("pipeline: map runs overlap or leave the map at entry %ld", e);
+                return 1;
+            }
+            p.plan_stamp[(size_t)e] = gen;
+            p.plan_map[(size_t)e] = m.value < 0 ? -1L : (long)m.value + j;
+        }
+    }
+    return 0;
+}
+
+// A whole layer: host plans of every frame, one staging launch (the copies
+// and map runs), one attention launch. Plan-only pipelines apply the staging
+// on the host instead and launch nothing.
 int run_layer(Pipeline& p, const char* q, const char* k, const char* v, char* out,
               const float* scores_flat) {
     p.next_frame = 0;
-    if (p.plan_only) {
-        for (int f = 0; f < p.frames; ++f) {
-            const int rc = step_frame(p, f, q, k, v, out, scores_flat);
-            if (rc) return rc;
-        }
-        return 0;
-    }
     if (!check_data(p, q, k, v, out)) return 1;
     if (!p.persist) {
         p.count = 0;
         p.staged_tiles = 0;
         p.copy_rows = 0;
-        return layer_attention(p, q, k, v, out);
+        return p.plan_only ? 0 : layer_attention(p, q, k, v, out);
     }
     if (layer_setup(p)) return 1;
+    p.last_mgr = p.layer_mgr.get();
+    ++p.layer_gen;
+    p.layer_nphys = 0;
     p.layer_copies.clear();
-    p.upd_rows.clear();
-    p.upd_vals.clear();
+    p.layer_updates.clear();
     for (int f = 0; f < p.frames; ++f) {
-        if (plan_frame_host(p, *p.layer_mgr, f, k, v, scores_flat)) return 1;
-        layer_collect(p, f, k, v);
+        if (select_and_release(p, *p.layer_mgr, f, scores_flat)) return 1;
+        plan_frame_layer(p, *p.layer_mgr, f, k, v);
+        if (layer_collect(p, f)) return 1;
         finish_frame(p, *p.layer_mgr, f);
     }
-    if (!p.layer_copies.empty() || !p.upd_rows.empty()) {
-        if (kvp_stage_run(p.layer_stager, p.layer_arena, 2L * p.D * p.elem, p.layer_copies.data(),
-                          (long)p.layer_copies.size(), p.layer_map, 0, p.upd_rows.data(),
-                          p.upd_vals.data(), (long)p.upd_rows.size(), p.stream))
-            return 1;
-    }
+    if (p.plan_only) return layer_apply_host(p);
+    if (layer_reserve(p)) return 1;
+    if (kvp::layer_stage_launch(p.layer_stager, p.layer_arena, k, v, (long)p.D * p.elem,
+                                p.layer_copies.data(), (long)p.layer_copies.size(), p.layer_map,
+                                p.layer_updates.data(), (long)p.layer_updates.size(), p.stream))
+        return 1;
     return layer_attention(p, q, k, v, out);
 }
 
@@ -575,7 +751,7 @@ long kvp_pipeline_map(void* p, long* out, long cap) {
 long kvp_pipeline_slots(void* p) { return PL(p)->slots; }
 long kvp_pipeline_staged_tiles(void* p) { return PL(p)->staged_tiles; }
 long kvp_pipeline_staged_bytes(void* p) {
-    return PL(p)->mgr ? (long)PL(p)->mgr->streaming_staged_bytes() : 0;
+    return PL(p)->last_mgr ? (long)PL(p)->last_mgr->streaming_staged_bytes() : 0;
 }
 long kvp_pipeline_copy_rows(void* p) { return PL(p)->copy_rows; }
 void* kvp_pipeline_arena(void* p) {
@@ -583,9 +759,25 @@ void* kvp_pipeline_arena(void* p) {
 }
 const long* kvp_pipeline_device_map(void* p) { return PL(p)->d_map; }
 void* kvp_pipeline_layer_arena(void* p) { return PL(p)->layer_arena; }
-long kvp_pipeline_layer_region_bytes(void* p) { return PL(p)->region_bytes; }
 const long* kvp_pipeline_layer_map(void* p) { return PL(p)->layer_map; }
 long kvp_pipeline_layer_map_stride(void* p) { return PL(p)->map_stride; }
+long kvp_pipeline_layer_copied_rows(void* p) { return PL(p)->layer_nphys; }
+
+long kvp_pipeline_layer_plan_map(void* p, int f, long* out, long cap) {
+    const Pipeline& pl = *PL(p);
+    if (!pl.plan_only || f < 0 || f >= pl.frames || pl.plan_map.empty()) return -1;
+    const long n = std::min(pl.map_stride, cap);
+    if (n > 0) memcpy(out, pl.plan_map.data() + (size_t)f * pl.map_stride, (size_t)n * sizeof(long));
+    return pl.map_stride;
+}
+
+long kvp_pipeline_layer_plan_sources(void* p, long* out, long cap) {
+    const Pipeline& pl = *PL(p);
+    if (!pl.plan_only) return -1;
+    const long n = std::min((long)pl.plan_src.size(), cap);
+    if (n > 0) memcpy(out, pl.plan_src.data(), (size_t)n * sizeof(long));
+    return (long)pl.plan_src.size();
+}
 void* kvp_pipeline_manager(void* p) { return PL(p)->mgr.get(); }
 
 }  // extern "C"

@@ -129,9 +129,11 @@ SIGNATURES = {
     "kvp_pipeline_device_map": (c_void_p, [c_void_p]),
     "kvp_pipeline_manager": (c_void_p, [c_void_p]),
     "kvp_pipeline_layer_arena": (c_void_p, [c_void_p]),
-    "kvp_pipeline_layer_region_bytes": (c_long, [c_void_p]),
     "kvp_pipeline_layer_map": (c_void_p, [c_void_p]),
     "kvp_pipeline_layer_map_stride": (c_long, [c_void_p]),
+    "kvp_pipeline_layer_copied_rows": (c_long, [c_void_p]),
+    "kvp_pipeline_layer_plan_map": (c_long, [c_void_p, c_int, c_long_p, c_long]),
+    "kvp_pipeline_layer_plan_sources": (c_long, [c_void_p, c_long_p, c_long]),
     # upstream K/V producer (reference: src/backbone.py:8-67), include/kvp_producer.h
     "kvp_layer_norm": (c_int, [c_int, c_int, c_void_p, c_void_p, c_void_p, c_void_p, c_long,
                                c_int, ctypes.c_float, c_void_p]),

@@ -356,8 +356,10 @@ class FramePipeline:
                                            self._scores), f"pipeline step {f}")
 
     def run(self, q=None, k=None, v=None, out=None) -> None:
-        """A whole layer: one staging launch for every frame's arena region and
-        KVMap slice, then one attention launch over all frames."""
+        """A whole layer: one staging launch that copies every row any frame
+        maps into the layer arena (once) and writes each frame's KVMap slice,
+        then one attention launch over all frames. Plan-only pipelines apply
+        the staging on the host (layer_plan_map / layer_plan_sources)."""
         _check(self._lib.kvp_pipeline_run(self._h, _ptr(q), _ptr(k), _ptr(v), _ptr(out),
                                           self._scores), "pipeline run")
 
@@ -391,13 +393,31 @@ class FramePipeline:
     def device_map_ptr(self) -> int:
         return int(self._lib.kvp_pipeline_device_map(self._h) or 0)
 
-    # layer mode (after run): frame f's arena region and KVMap slice
-    def layer_arena_ptr(self, f: int = 0) -> int:
-        base = int(self._lib.kvp_pipeline_layer_arena(self._h) or 0)
-        return base + f * int(self._lib.kvp_pipeline_layer_region_bytes(self._h)) if base else 0
+    # layer mode (after run): the arena all frames share, frame f's KVMap
+    # slice, and the rows the last run copied
+    def layer_arena_ptr(self) -> int:
+        return int(self._lib.kvp_pipeline_layer_arena(self._h) or 0)
 
-    def layer_region_bytes(self) -> int:
-        return int(self._lib.kvp_pipeline_layer_region_bytes(self._h))
+    def layer_copied_rows(self) -> int:
+        return int(self._lib.kvp_pipeline_layer_copied_rows(self._h))
+
+    # plan-only pipelines, after run(): the layer map slice of frame f and
+    # the K/V row of each physical row, as the staging launch would leave them
+    def layer_plan_map(self, f: int) -> np.ndarray:
+        n = int(self._lib.kvp_pipeline_layer_plan_map(self._h, f, None, 0))
+        if n < 0:
+            raise RuntimeError("layer_plan_map: not a plan-only pipeline after run()")
+        buf = np.empty(n, dtype=np.int64)
+        self._lib.kvp_pipeline_layer_plan_map(self._h, f, buf.ctypes.data_as(_lib.c_long_p), n)
+        return buf
+
+    def layer_plan_sources(self) -> np.ndarray:
+        n = int(self._lib.kvp_pipeline_layer_plan_sources(self._h, None, 0))
+        if n < 0:
+            raise RuntimeError("layer_plan_sources: not a plan-only pipeline after run()")
+        buf = np.empty(n, dtype=np.int64)
+        self._lib.kvp_pipeline_layer_plan_sources(self._h, buf.ctypes.data_as(_lib.c_long_p), n)
+        return buf
 
     def layer_map_ptr(self, f: int = 0) -> int:
         base = int(self._lib.kvp_pipeline_layer_map(self._h) or 0)

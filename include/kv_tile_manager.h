@@ -29,6 +29,8 @@
 //
 // Not thread-safe (same as the reference).
 
+#include <algorithm>
+#include <climits>
 #include <cstddef>
 #include <unordered_map>
 #include <vector>
@@ -43,6 +45,86 @@ enum KvtmResult {
 
 // Residency ceiling used by init(): gfx950 Infinity Cache (256 MiB).
 static const size_t KVTM_RESIDENCY_LIMIT_BYTES = (size_t)256 << 20;
+
+// Row id -> arena slot table of the streaming mode: open addressing with
+// linear probing over a power-of-two array; erased entries leave tombstones
+// that later inserts reuse, and the table is rebuilt when entries plus
+// tombstones pass half of it. Keys kEmpty and kTomb mark free entries, so
+// any row id but the two smallest longs can be stored. An implementation
+// detail of KVTileManager, kept here because the class holds one.
+class KvtmRowTable {
+public:
+    static constexpr long kEmpty = LONG_MIN;
+    static constexpr long kTomb = LONG_MIN + 1;
+    // Slot of row, or -1 when absent (slots are >= 0).
+    long find(long row) const {
+        if (keys_.empty()) return -1;
+        for (size_t i = home(row);; i = (i + 1) & mask_) {
+            if (keys_[i] == row) return vals_[i];
+            if (keys_[i] == kEmpty) return -1;
+        }
+    }
+    void insert(long row, long slot) {  // row must be absent
+        if ((size_ + tombs_ + 1) * 2 > keys_.size()) rebuild();
+        size_t i = home(row);
+        while (keys_[i] != kEmpty && keys_[i] != kTomb) i = (i + 1) & mask_;
+        if (keys_[i] == kTomb) --tombs_;
+        keys_[i] = row;
+        vals_[i] = slot;
+        ++size_;
+    }
+    // Removes row; returns its slot, or -1 when absent.
+    long erase(long row) {
+        if (keys_.empty()) return -1;
+        for (size_t i = home(row);; i = (i + 1) & mask_) {
+            if (keys_[i] == row) {
+                keys_[i] = kTomb;
+                --size_;
+                ++tombs_;
+                return vals_[i];
+            }
+            if (keys_[i] == kEmpty) return -1;
+        }
+    }
+    void clear() {
+        std::fill(keys_.begin(), keys_.end(), kEmpty);
+        size_ = 0;
+        tombs_ = 0;
+    }
+    void reserve(size_t n) {
+        if ((n + tombs_) * 2 > keys_.size()) rebuild(n);
+    }
+    size_t size() const { return size_; }
+
+private:
+    // Row ids are mostly dense (frame * T + token): consecutive ids take
+    // consecutive buckets, so a tile's rows probe one or two cache lines;
+    // the folded high bits break up ids that differ by a power of two.
+    size_t home(long row) const {
+        const unsigned long long r = (unsigned long long)row;
+        return (size_t)(r ^ (r >> 17) ^ (r >> 34)) & mask_;
+    }
+    // Re-inserts the live entries into a table with room for at least
+    // `want` of them at half load (tombstones dropped).
+    void rebuild(size_t want = 0) {
+        size_t cap = 64;
+        while (cap < 4 * (size_ + 1) || cap < 2 * want) cap *= 2;
+        std::vector<long> ok, ov;
+        ok.swap(keys_);
+        ov.swap(vals_);
+        keys_.assign(cap, kEmpty);
+        vals_.assign(cap, 0);
+        mask_ = cap - 1;
+        size_ = 0;
+        tombs_ = 0;
+        for (size_t i = 0; i < ok.size(); ++i)
+            if (ok[i] != kEmpty && ok[i] != kTomb) insert(ok[i], ov[i]);
+    }
+    std::vector<long> keys_, vals_;
+    size_t mask_ = 0;
+    size_t size_ = 0;
+    size_t tombs_ = 0;
+};
 
 class KVTileManager {
 public:
@@ -110,6 +192,18 @@ public:
     // manager is plan-only). The pending copies are handed over at once.
     bool flush_plan(void** plan, long* map_dev, long map_fill, const long* map_rows,
                     const long* map_slots, size_t n_map) const;
+    // Batched staging of n consecutive rows, row i's K at k_first + i*k_bytes
+    // and V at v_first + i*v_bytes (null bases stay null): the decisions and
+    // state of n calls of arena_stage, or of streaming_stage with row ids
+    // row_first + i and changed = false, made in row order and stopped at the
+    // first refusal. Returns the rows staged; their slots go to out_slots
+    // when it is non-null. *copied receives the staged rows that needed a
+    // copy (every row in arena mode; no sticky hits in streaming mode).
+    long arena_stage_rows(const char* k_first, size_t k_bytes, const char* v_first,
+                          size_t v_bytes, long n, long* out_slots);
+    long streaming_stage_rows(long row_first, const char* k_first, size_t k_bytes,
+                              const char* v_first, size_t v_bytes, long n,
+                              long* out_slots, long* copied);
 
 private:
     bool record_copy(long dst_row, const void* k_dev, size_t k_bytes,
@@ -136,7 +230,7 @@ private:
     size_t arena_next_row_;
     size_t arena_used_;
 
-    std::unordered_map<long, long> row_slot_;
+    KvtmRowTable row_slot_;
     std::vector<long> free_slots_;
     long slot_high_water_;
     size_t staged_bytes_;

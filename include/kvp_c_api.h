@@ -245,13 +245,19 @@ int kvp_pipeline_step(void* p, int f, const void* q, const void* k,
                       const void* v, void* out, const float* scores_flat);
 /* A whole layer, frames 0..frames-1 (streaming state is reset first), in
  * two launches: every frame's host plan is made first, then one staging
- * launch writes frame f's arena state to region f of a layer arena (every row
- * frame f's map points to, at its slot) and frame f's KVMap to slice f of a
- * layer map, then one attention launch runs all frames, frame f reading its
- * own region and slice. Outputs equal frame-by-frame stepping bit for bit.
- * The layer arena is frames x (set_aside rounded down to whole rows) bytes;
- * the layer map holds frames slices of frames*T (cross) or T (intra)
- * entries, absolute key rows in cross mode, frame-relative in intra mode. */
+ * launch copies every row any frame maps into a layer arena, once per row
+ * (physical rows in first-mapped order; K and V are fixed for the layer, so
+ * the copy serves every frame that maps the row), and writes frame f's
+ * KVMap to slice f of a layer map, pointing each row frame f maps at its
+ * physical row; then one attention launch runs all frames, frame f reading
+ * its own slice. Each frame maps exactly the rows frame-by-frame stepping
+ * maps, so outputs equal stepping bit for bit. The layer arena holds
+ * min(frames x rows-per-set-aside, frames*T) rows of [K | V]; the layer map
+ * holds frames slices of frames*T (cross) or T (intra) entries, absolute key
+ * rows in cross mode, frame-relative in intra mode. A plan-only pipeline
+ * makes the same plans and applies the staging launch's runs to host copies
+ * of the map and of each physical row's source row, launching nothing
+ * (kvp_pipeline_layer_plan_map / _plan_sources). */
 int kvp_pipeline_run(void* p, const void* q, const void* k, const void* v,
                      void* out, const float* scores_flat);
 /* Introspection of the last step. */
@@ -265,12 +271,19 @@ long kvp_pipeline_copy_rows(void* p);
 void* kvp_pipeline_arena(void* p);
 const long* kvp_pipeline_device_map(void* p);
 void* kvp_pipeline_manager(void* p);
-/* Layer mode (kvp_pipeline_run): region f at arena + f*region_bytes,
- * slice f at map + f*map_stride entries; NULL / 0 before the first run. */
+/* Layer mode (kvp_pipeline_run): the arena every frame reads, slice f at
+ * map + f*map_stride entries, and the rows the last run copied into the
+ * arena; NULL / 0 before the first run. */
 void* kvp_pipeline_layer_arena(void* p);
-long kvp_pipeline_layer_region_bytes(void* p);
 const long* kvp_pipeline_layer_map(void* p);
 long kvp_pipeline_layer_map_stride(void* p);
+long kvp_pipeline_layer_copied_rows(void* p);
+/* Plan-only pipelines, after kvp_pipeline_run: slice f of the layer map
+ * (returns map_stride, copies min(map_stride, cap) entries) and the K/V row
+ * each physical row holds (returns the row count, copies min(count, cap));
+ * -1 for pipelines that are not plan-only or before the first run. */
+long kvp_pipeline_layer_plan_map(void* p, int f, long* out, long cap);
+long kvp_pipeline_layer_plan_sources(void* p, long* out, long cap);
 
 #ifdef __cplusplus
 }

@@ -164,14 +164,14 @@ def test_c5_shape_single_frame_pair_bf16():
     assert float((base.float().cpu()[T:T + 128] - want).abs().max()) <= 2e-2
 
 
-def _layer_region(pl, f, rows, dtype):
+def _layer_arena(pl, rows, dtype):
     n = rows * 2 * D
     buf = torch.empty(n, dtype=dtype, device=DEV)
     esz = 4 if dtype == torch.float32 else 2
     from kvpersist import _lib
     lib = _lib.load()
     torch.cuda.synchronize()
-    assert lib.kvp_memcpy_d2d(buf.data_ptr(), pl.layer_arena_ptr(f), n * esz, None) == 0
+    assert lib.kvp_memcpy_d2d(buf.data_ptr(), pl.layer_arena_ptr(), n * esz, None) == 0
     torch.cuda.synchronize()
     return buf.view(rows, 2 * D)
 
@@ -187,13 +187,16 @@ def _layer_map(pl, f, n):
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 @pytest.mark.parametrize("streaming", [False, True])
-def test_run_layer_regions_and_maps_match_oracle_plan(dtype, streaming):
-    """kvp_pipeline_run stages every frame's arena state into its own region
-    and its KVMap into its own slice, then runs all frames in one launch.
-    After the run, slice f must equal the oracle driver's map of frame f and
-    region f must hold [K row | V row] at every slot that map points to;
-    outputs are bitwise equal to policy none run the same way, and within
-    the dtype's bar of frame-by-frame stepping (which may split key ranges)."""
+def test_run_layer_arena_and_maps_match_oracle_plan(dtype, streaming):
+    """kvp_pipeline_run copies every row any frame of the layer maps into one
+    layer arena, once, and writes frame f's KVMap to slice f of a layer map,
+    then runs all frames in one launch. After the run, slice f must map
+    exactly the rows the oracle driver's map of frame f maps, each to a
+    distinct physical row holding [K row | V row]; a row keeps one physical
+    row across frames; the copied rows are the union of the frames' mapped
+    rows. Outputs are bitwise equal to policy none run the same way, and
+    within the dtype's bar of frame-by-frame stepping (which may split key
+    ranges)."""
     cfg = workloads.CONFIGS["c3"]
     frames, T = 4, cfg.tokens
     qkv = _device_inputs(frames, T, dtype, seed=9)
@@ -224,21 +227,30 @@ def test_run_layer_regions_and_maps_match_oracle_plan(dtype, streaming):
                                   D=D, tile_tokens=16, set_aside=set_aside, elem=elem,
                                   scores_flat=scores)
             assert pl.layer_map_stride() == frames * T
-            rows_per_region = set_aside // (2 * D * elem)
-            assert pl.layer_region_bytes() == rows_per_region * 2 * D * elem
+            union = set()
+            for f in range(frames):
+                union.update(np.nonzero(plan[f]["map"] >= 0)[0].tolist())
+            copied = pl.layer_copied_rows()
+            assert copied == len(union)
+            arena = _layer_arena(pl, copied, dtype)
             kflat, vflat = kd.view(frames * T, D), vd.view(frames * T, D)
+            phys_of = {}
             for f in range(frames):
                 dmap = _layer_map(pl, f, frames * T)
-                np.testing.assert_array_equal(dmap[:(f + 1) * T], plan[f]["map"],
-                                              err_msg=f"map slice {f}")
+                want = plan[f]["map"]
+                np.testing.assert_array_equal(dmap[:(f + 1) * T] >= 0, want >= 0,
+                                              err_msg=f"mapped rows of slice {f}")
                 assert (dmap[(f + 1) * T:] == -1).all(), f
                 rows = np.nonzero(dmap >= 0)[0]
                 assert rows.size > 0
-                region = _layer_region(pl, f, rows_per_region, dtype)
-                slots = torch.from_numpy(dmap[rows]).to(DEV)
+                phys = dmap[rows]
+                assert phys.max() < copied and np.unique(phys).size == phys.size, f
+                for r, ph in zip(rows.tolist(), phys.tolist()):
+                    assert phys_of.setdefault(r, ph) == ph, (f, r)
+                pidx = torch.from_numpy(phys).to(DEV)
                 ridx = torch.from_numpy(rows).to(DEV)
-                assert torch.equal(region[slots, :D], kflat[ridx]), f
-                assert torch.equal(region[slots, D:], vflat[ridx]), f
+                assert torch.equal(arena[pidx, :D], kflat[ridx]), f
+                assert torch.equal(arena[pidx, D:], vflat[ridx]), f
         pl.close()
     assert torch.equal(outs["motion"], outs["none"])
     tol = 2e-5 if dtype == torch.float32 else 1.6e-2
