@@ -18,6 +18,11 @@
 // descriptors straight from a ring of mapped pinned host memory (no separate
 // H2D copy); a ring region is reused only after the event recorded behind
 // the launch that read it has completed.
+//
+// Layer staging (the frame pipeline's whole-layer run) has its own kernel:
+// run tables of up to ~24 KiB row copies and up to 1024-entry map runs, one
+// workgroup per run, read from the same ring; every thread moves 16-byte
+// chunks with four loads in flight.
 
 #include <hip/hip_runtime.h>
 
