@@ -517,6 +517,18 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_bf16_kernel(AttnArgs a) 
     // frame's keys), and then neither the per-row decode nor the per-lane
     // choice of source runs: the wave copies like the map-free kernel.
     bool grp_mapped = false;
+    // Wave-uniform: every row of the group maps into the arena, to
+    // consecutive arena rows (a run; arena byte offset run_base for the
+    // group's first row). Such a group copies like a plain group, its K and
+    // V descriptors based at that arena row (the frame pipeline's layer
+    // arena holds mapped tiles in key order, so most fully mapped groups are
+    // runs). Not in the non-temporal variant, whose hint must reach original
+    // rows only.
+    constexpr bool kRuns = kMap && !kColdNt;
+    bool grp_run = false;
+    unsigned run_base = 0;
+    // arena byte offset of the lane's first copy row within a run
+    const unsigned lane_arena = 2u * (unsigned)(lane >> 4) * rb;
     // Dword 2e+1 of a wave's map slot is the high word of its group's entry e
     // (row 16*wave + e); an entry can name an arena row only when that word is
     // 0. Each lane reads one dword of the slot of the next tile to decode
@@ -536,6 +548,7 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_bf16_kernel(AttnArgs a) 
         lgkm_wait1(hw);
         grp_mapped = __builtin_amdgcn_ballot_w64(lane < 32 && (lane & 1) && hw == 0u &&
                                                  16 * wave + (lane >> 1) < valid_rows) != 0;
+        grp_run = false;
         if (!grp_mapped) {
 #pragma unroll
             for (int i = 0; i < 4; ++i) mdec[i] = ~0u;
@@ -550,6 +563,17 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_bf16_kernel(AttnArgs a) 
             mdec[i] = (ld_row0 + 4 * i < valid_rows && mw[i][1] == 0u && mw[i][0] <= max_arena_row)
                           ? 2u * mw[i][0] * rb
                           : ~0u;
+        // a run: row 4i + lane/16 of the group at run_base + that row's offset
+        // (lane 0 holds row 0; an unmapped row never matches, ~0u being odd
+        // and every arena offset even)
+        if constexpr (kRuns) {
+            run_base = (unsigned)__builtin_amdgcn_readfirstlane((int)mdec[0]);
+            bool ok = run_base != ~0u;
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                ok = ok && mdec[i] == run_base + lane_arena + 8u * (unsigned)i * rb;
+            grp_run = __builtin_amdgcn_ballot_w64(!ok) == 0;
+        }
     };
     auto load_map = [&](int t) {
         if constexpr (!kMap) return;
@@ -571,6 +595,9 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_bf16_kernel(AttnArgs a) 
     // computed, so the copies trickle out between MFMAs.
     __amdgpu_buffer_rsrc_t krs, vrs;
     unsigned koff = 0, voff = 0;
+    // copy_plain's per-lane offsets: copy i reads K at cp_k + i*cp_step +
+    // kofs[i] and V at cp_v + i*cp_step + vofs through krs / vrs
+    unsigned cp_k = lane_row, cp_v = lane_row, cp_step = 4u * rb;
     auto prep_tile = [&](int t, unsigned char* kdst, unsigned char* vdst) {
         const long t0 = kbeg + (long)t * kBf16BlockKeys;
         const long left = kend - t0;
@@ -583,6 +610,18 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_bf16_kernel(AttnArgs a) 
                                                 (short)0, nrec, kBufFlags);
         koff = (unsigned)__builtin_amdgcn_readfirstlane((int)(uintptr_t)kdst) + 4096u * wave;
         voff = (unsigned)__builtin_amdgcn_readfirstlane((int)(uintptr_t)vdst) + 4096u * wave;
+        cp_k = lane_row;
+        cp_v = lane_row;
+        cp_step = 4u * rb;
+        if (kRuns && grp_run) {
+            // [K row | V row] arena rows of the run: 2*rb apart, V rb after K
+            krs = __builtin_amdgcn_make_buffer_rsrc(
+                const_cast<unsigned char*>(Ab + run_base), (short)0, -1, kBufFlags);
+            vrs = krs;
+            cp_k = lane_arena;
+            cp_v = lane_arena + rb;
+            cp_step = 8u * rb;
+        }
     };
     auto copy_pair = [&](int i) {
         KVP_LDS void* kd = (KVP_LDS void*)(uintptr_t)(koff + 1024u * i);
@@ -600,24 +639,24 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_bf16_kernel(AttnArgs a) 
         }
     };
     // The copies interleaved with the QK MFMAs: the map-free kernel's copies
-    // (no per-lane source choice, no branch between the MFMAs). For a group
-    // with arena rows, whose copies were issued before the tile (copy_pair),
-    // they land in the wave's sink instead (scalar select of the LDS target
-    // and the descriptor).
+    // (no per-lane source choice, no branch between the MFMAs), from the
+    // arena for a run. For a group mixing arena and original rows, whose
+    // copies were issued before the tile (copy_pair), they land in the wave's
+    // sink instead (scalar select of the LDS target and the descriptor).
     const unsigned sink = (unsigned)(uintptr_t)sink_lds + 2048u * (unsigned)wave;
     // A sinked copy goes through a descriptor of zero records: it reads
     // nothing from memory (out-of-range loads return zeros).
     const __amdgpu_buffer_rsrc_t empty_rs =
         __builtin_amdgcn_make_buffer_rsrc(const_cast<unsigned char*>(Kb), (short)0, 0, kBufFlags);
     auto copy_plain = [&](int i) {
-        const bool to_sink = kMap && grp_mapped;
+        const bool to_sink = kMap && grp_mapped && !(kRuns && grp_run);
         KVP_LDS void* kd = (KVP_LDS void*)(uintptr_t)(to_sink ? sink : koff + 1024u * i);
         KVP_LDS void* vd = (KVP_LDS void*)(uintptr_t)(to_sink ? sink + 1024u : voff + 1024u * i);
         const __amdgpu_buffer_rsrc_t ks = to_sink ? empty_rs : krs;
         const __amdgpu_buffer_rsrc_t vs = to_sink ? empty_rs : vrs;
-        const unsigned row_off = lane_row + 4u * i * rb;
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(ks, kd, 16, row_off + kofs[i], 0, 0, kColdAux);
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(vs, vd, 16, row_off + vofs, 0, 0, kColdAux);
+        const unsigned step = (unsigned)i * cp_step;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(ks, kd, 16, cp_k + step + kofs[i], 0, 0, kColdAux);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(vs, vd, 16, cp_v + step + vofs, 0, 0, kColdAux);
     };
 
     f32x16 o[4];
@@ -842,14 +881,15 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_bf16_kernel(AttnArgs a) 
             if (kMap && t + 2 < ntiles) load_map(t + 2);
         } else if (kMap) {
             grp_mapped = false;
+            grp_run = false;
 #pragma unroll
             for (int i = 0; i < 4; ++i) mdec[i] = ~0u;
         }
         prep_tile(t + 1, knext, vnext);
-        if (!active || (kMap && grp_mapped)) {
-            // inactive waves, and groups with arena rows (rare; wave-uniform):
-            // each row's source chosen per lane, copies issued before the
-            // tile's MFMAs
+        if (!active || (kMap && grp_mapped && !(kRuns && grp_run))) {
+            // inactive waves, and groups mixing arena and original rows
+            // (wave-uniform): each row's source chosen per lane, copies
+            // issued before the tile's MFMAs
 #pragma unroll
             for (int i = 0; i < 4; ++i) copy_pair(i);
         }

@@ -93,14 +93,14 @@ struct Pipeline {
         long gsrc;
         int n;
     };
-    std::vector<Seg> segs;                     // the frame being planned
+    std::vector<std::vector<Seg>> frame_segs;  // per frame: its segments this run
     std::vector<std::vector<int>> seg_n;       // per frame: rows mapped per tile on the device
     std::vector<std::vector<long>> seg_phys;   // per frame: their first physical row
     std::vector<std::vector<long>> seg_list;   // per frame: tiles with seg_n > 0
     std::vector<int> seg_mark;                 // tile idx -> frame plan that maps it
     int seg_gen = 0;
     std::vector<long> tile_phys;               // gsrc -> first physical row this run
-    std::vector<int> tile_gen;                 // run that set tile_phys
+    std::vector<int> tile_gen;                 // run that last mapped the tile
     int layer_gen = 0;
     long layer_nphys = 0;                      // physical rows assigned this run
     std::vector<long> tile_slots;              // slots of one tile (host map)
@@ -376,6 +376,7 @@ int layer_setup(Pipeline& p) {
     p.map_stride = p.cross ? (long)p.frames * p.T : (long)p.T;
     p.seg_space = p.cross ? (long)p.frames * p.num_tiles : p.num_tiles;
     const long map_entries = (long)p.frames * p.map_stride;
+    p.frame_segs.assign((size_t)p.frames, {});
     p.seg_n.assign((size_t)p.frames, std::vector<int>((size_t)p.seg_space, 0));
     p.seg_phys.assign((size_t)p.frames, std::vector<long>((size_t)p.seg_space, -1L));
     p.seg_list.assign((size_t)p.frames, {});
@@ -406,7 +407,8 @@ int layer_setup(Pipeline& p) {
 // Step 3 of a gated frame in layer mode, a tile at a time: the manager
 // takes the decisions of plan_frame_host's row loop (batched per tile, same
 // order, same stop at a tile's first refused row), and the frame's mapped
-// rows are kept as segments in p.segs. The host map is written for the last
+// rows are kept as segments in p.frame_segs[f] (and their tiles marked as
+// mapped this run). The host map is written for the last
 // frame of the layer only (introspection of the last step).
 void plan_frame_layer(Pipeline& p, KVTileManager& mgr, int f, const char* k, const char* v) {
     const long T = p.T;
@@ -414,7 +416,8 @@ void plan_frame_layer(Pipeline& p, KVTileManager& mgr, int f, const char* k, con
     const bool last = f + 1 == p.frames;
     mgr.arena_begin_step();
     if (last) std::fill(p.h_map.begin(), p.h_map.begin() + (size_t)(f + 1) * T, -1L);
-    p.segs.clear();
+    std::vector<Pipeline::Seg>& segs = p.frame_segs[(size_t)f];
+    segs.clear();
     p.staged_tiles = 0;
     p.copy_rows = 0;
     for (int i = 0; i < p.count; ++i) {
@@ -442,20 +445,38 @@ void plan_frame_layer(Pipeline& p, KVTileManager& mgr, int f, const char* k, con
         if (last)
             for (long j = 0; j < n; ++j) p.h_map[(size_t)(row0 + j)] = p.tile_slots[(size_t)j];
         if (n == c) ++p.staged_tiles;
-        if (n > 0)
-            p.segs.push_back(Pipeline::Seg{p.cross ? src_f * p.num_tiles + tile : tile,
-                                           src_f * p.num_tiles + tile, (int)n});
+        if (n > 0) {
+            const long gsrc = src_f * p.num_tiles + tile;
+            segs.push_back(Pipeline::Seg{p.cross ? gsrc : tile, gsrc, (int)n});
+            p.tile_gen[(size_t)gsrc] = p.layer_gen;
+        }
     }
 }
 
 // Copy of c K/V rows from row `row` to physical rows [phys, phys + c),
-// appended to the run table in runs of at most ~24 KiB.
+// appended to the run table: runs of consecutive rows (also across tiles)
+// of at most ~24 KiB each.
 void layer_add_copy(Pipeline& p, long row, long phys, long c) {
     const long row_bytes = 2L * p.D * p.elem;
     const long per_run = std::max<long>(1, std::min<long>(kvp::kLayerCopyRows, 24576 / row_bytes));
-    for (long j = 0; j < c; j += per_run)
-        p.layer_copies.push_back(kvp::LayerCopyRun{(int)(row + j), (int)(phys + j),
-                                                   (int)std::min(per_run, c - j), 0});
+    while (c > 0) {
+        if (!p.layer_copies.empty()) {
+            kvp::LayerCopyRun& r = p.layer_copies.back();
+            if (r.n < per_run && r.src_row + r.n == row && r.dst_row + r.n == phys) {
+                const long k = std::min(c, per_run - r.n);
+                r.n += (int)k;
+                row += k;
+                phys += k;
+                c -= k;
+                continue;
+            }
+        }
+        const long k = std::min(c, per_run);
+        p.layer_copies.push_back(kvp::LayerCopyRun{(int)row, (int)phys, (int)k, 0});
+        row += k;
+        phys += k;
+        c -= k;
+    }
 }
 
 // Map entries [index, index + n) set to value + j (value -1: reset).
@@ -466,33 +487,46 @@ void layer_add_update(Pipeline& p, long index, long value, long n) {
             (int)std::min<long>(kvp::kLayerMapEntries, n - j)});
 }
 
-// Frame f's share of the layer staging launch: physical rows (and their
-// copy) for every tile the frame maps that has none yet this run, a whole
-// tile each, and the runs of map slice f that differ from what the device
-// holds. Write runs cover the rows a tile maps now; reset runs only rows
-// no tile of the frame maps now, so the runs of one launch never overlap.
-int layer_collect(Pipeline& p, int f) {
+// Physical rows of the run: every tile some frame maps, a whole tile each,
+// in key order (tile id order is key-row order, across frames too), so the
+// arena rows of adjacent mapped tiles are adjacent and a 16-row copy group
+// of the attention kernel whose rows are all mapped is one run of arena
+// rows. One copy run table for all of them.
+int layer_assign(Pipeline& p) {
+    const long T = p.T;
+    const long ntiles = (long)p.frames * p.num_tiles;
+    for (long g = 0; g < ntiles; ++g) {
+        if (p.tile_gen[(size_t)g] != p.layer_gen) continue;
+        const long tile = g % p.num_tiles;
+        const long row0 = (g / p.num_tiles) * T + tile * p.tile_tokens;
+        const long c = std::min((long)p.tile_tokens, T - tile * p.tile_tokens);
+        if (p.layer_nphys + c > 0x7fffffffL || row0 + c > 0x7fffffffL) {
+            kvp::set_error("pipeline: layer arena rows exceed int");
+            return 1;
+        }
+        p.tile_phys[(size_t)g] = p.layer_nphys;
+        layer_add_copy(p, row0, p.layer_nphys, c);
+        p.layer_nphys += c;
+    }
+    return 0;
+}
+
+// Frame f's map runs: the entries of map slice f that differ from what the
+// device holds. Write runs cover the rows a tile maps now; reset runs only
+// rows no tile of the frame maps now, so the runs of one launch never
+// overlap.
+void layer_collect(Pipeline& p, int f) {
     const long T = p.T;
     const long base = (long)f * p.map_stride;
     const long rel = p.cross ? 0 : (long)f * T;  // intra slices are frame-relative
     std::vector<int>& sn = p.seg_n[(size_t)f];
     std::vector<long>& sp = p.seg_phys[(size_t)f];
     std::vector<long>& list = p.seg_list[(size_t)f];
+    const std::vector<Pipeline::Seg>& segs = p.frame_segs[(size_t)f];
     ++p.seg_gen;
-    for (const Pipeline::Seg& s : p.segs) {
+    for (const Pipeline::Seg& s : segs) {
         const long tile = s.gsrc % p.num_tiles;
         const long row0 = (s.gsrc / p.num_tiles) * T + tile * p.tile_tokens;
-        if (p.tile_gen[(size_t)s.gsrc] != p.layer_gen) {
-            const long c = std::min((long)p.tile_tokens, T - tile * p.tile_tokens);
-            if (p.layer_nphys + c > 0x7fffffffL || row0 + c > 0x7fffffffL) {
-                kvp::set_error("pipeline: layer arena rows exceed int");
-                return 1;
-            }
-            p.tile_gen[(size_t)s.gsrc] = p.layer_gen;
-            p.tile_phys[(size_t)s.gsrc] = p.layer_nphys;
-            layer_add_copy(p, row0, p.layer_nphys, c);
-            p.layer_nphys += c;
-        }
         const long ph = p.tile_phys[(size_t)s.gsrc];
         const long e0 = base + row0 - rel;
         const int old_n = sn[(size_t)s.idx];
@@ -509,12 +543,11 @@ int layer_collect(Pipeline& p, int f) {
         sp[(size_t)idx] = -1;
     }
     list.clear();
-    for (const Pipeline::Seg& s : p.segs) {
+    for (const Pipeline::Seg& s : segs) {
         sn[(size_t)s.idx] = s.n;
         sp[(size_t)s.idx] = p.tile_phys[(size_t)s.gsrc];
         list.push_back(s.idx);
     }
-    return 0;
 }
 
 // Grow the layer arena to hold the run's physical rows (rare: a layer with
@@ -625,9 +658,10 @@ int run_layer(Pipeline& p, const char* q, const char* k, const char* v, char* ou
     for (int f = 0; f < p.frames; ++f) {
         if (select_and_release(p, *p.layer_mgr, f, scores_flat)) return 1;
         plan_frame_layer(p, *p.layer_mgr, f, k, v);
-        if (layer_collect(p, f)) return 1;
         finish_frame(p, *p.layer_mgr, f);
     }
+    if (layer_assign(p)) return 1;
+    for (int f = 0; f < p.frames; ++f) layer_collect(p, f);
     if (p.plan_only) return layer_apply_host(p);
     if (layer_reserve(p)) return 1;
     if (kvp::layer_stage_launch(p.layer_stager, p.layer_arena, k, v, (long)p.D * p.elem,

@@ -125,6 +125,58 @@ def test_kvmap_with_key_splits_is_bitwise_invisible(dtype):
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_kvmap_group_shapes_bitwise_invisible(dtype):
+    """The bf16 kernel copies a 16-row group whose rows all map to
+    consecutive arena rows (a run) like an unmapped group, from the arena;
+    every other mapped group chooses each row's source per lane. Groups of
+    every shape the run check tells apart — unmapped, run, run from arena
+    row 0, reversed, a run with one hole (row 5, or row 0), a jump between
+    two halves, a jump at a 4-row boundary, and a partial last group — must
+    give the map-free output bit for bit; arena rows no entry names hold
+    NaN, so a wrong read would show."""
+    frames, T, heads = 1, 680, 2
+    D = heads * 128
+    q, k, v = _inputs(frames, T, heads, seed=21, dtype=dtype)
+    base = _run(dtype, q, k, v, frames, T, heads, "cross")
+    kvmap = torch.full((T,), -1, dtype=torch.int64)
+    nxt = 16  # arena rows 0..15 belong to the first run based at row 0
+    zero_used = False
+    for g in range((T + 15) // 16):
+        rows = list(range(16 * g, min(16 * g + 16, T)))
+        n, pat = len(rows), g % 8
+        if pat == 0:
+            continue
+        if pat == 7 and not zero_used:
+            b, zero_used = 0, True
+        else:
+            b = nxt
+            nxt += n + 128
+        slots = [b + j for j in range(n)]
+        if pat == 2:
+            slots = slots[::-1]
+        elif pat == 3 and n > 5:
+            slots[5] = -1
+        elif pat == 4:
+            slots[0] = -1
+        elif pat == 5:
+            slots = [b + j + (50 if j >= 8 else 0) for j in range(n)]
+        elif pat == 6:
+            slots = [b + j + (100 if j >= 4 else 0) for j in range(n)]
+        for r, s in zip(rows, slots):
+            kvmap[r] = s
+    arena = torch.full((nxt, 2 * D), float("nan"), dtype=dtype)
+    kt, vt = k.to(dtype), v.to(dtype)
+    for r in range(T):
+        s = int(kvmap[r])
+        if s >= 0:
+            arena[s, :D] = kt[r]
+            arena[s, D:] = vt[r]
+    got = _run(dtype, q, k, v, frames, T, heads, "cross", arena=arena.to(DEV).contiguous(),
+               kvmap=kvmap.to(DEV))
+    assert torch.equal(got, base)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 def test_kvmap_entries_outside_arena_rows_read_original(dtype):
     """Negative entries of any value read the original K/V row, valid entries
     their arena row. bf16 also: entries whose arena row would end beyond the

@@ -12,8 +12,8 @@ entry twice. For every frame f of the layer:
   * each mapped row points at a physical row whose source is that row, rows
     of one frame at distinct physical rows;
 a row keeps one physical row across the layer, physical rows are handed out
-a whole tile at a time (the copied rows are the rows of every tile some
-frame maps), and the last frame's introspection (selected ids, staged tiles,
+a whole tile at a time in key order (the copied rows are the rows of every
+tile some frame maps, ascending), and the last frame's introspection (selected ids, staged tiles,
 rows copied, slot map, streaming bytes) equals the oracle's. Layers are run
 back to back with different scores, so the map runs also cover entries that
 change or go back to -1 between runs.
@@ -75,10 +75,11 @@ def _check_layer(pl, policy, *, cross, streaming, frames, T, set_aside, elem, sc
         for r, ph in zip((rows + rows0).tolist(), phys.tolist()):
             assert phys_of.setdefault(r, ph) == ph, (f, r)
             touched.add(r // T * ((T + TILE - 1) // TILE) + (r % T) // TILE)
-    # whole tiles: each touched tile's rows, once
+    # whole tiles: each touched tile's rows, once, in key order (so the rows
+    # of adjacent mapped tiles sit in adjacent arena rows)
     rows_of = {g: min(TILE, T - (g % ((T + TILE - 1) // TILE)) * TILE) for g in touched}
     assert src.size == sum(rows_of.values())
-    assert np.unique(src).size == src.size
+    assert (np.diff(src) > 0).all()
 
 
 CASES = [
