@@ -554,6 +554,23 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_bf16_kernel(AttnArgs a) 
             for (int i = 0; i < 4; ++i) mdec[i] = ~0u;
             return;
         }
+        if constexpr (kRuns) {
+            // Lanes 0-31 already hold the group's 16 entries (entry e: low
+            // word in lane 2e, high word in lane 2e+1). A run: all 16 rows
+            // inside the range, every high word 0, low words l0 .. l0+15 with
+            // the last row inside the reach of 32-bit offsets; then no
+            // per-row decode.
+            const unsigned l0 = (unsigned)__builtin_amdgcn_readlane((int)hw, 0);
+            const bool full = 16 * wave + 16 <= valid_rows && l0 <= max_arena_row - 15u;
+            const bool ok = lane >= 32 || ((lane & 1) ? hw == 0u : hw == l0 + (unsigned)(lane >> 1));
+            if (full && __builtin_amdgcn_ballot_w64(!ok) == 0) {
+                grp_run = true;
+                run_base = 2u * l0 * rb;
+#pragma unroll
+                for (int i = 0; i < 4; ++i) mdec[i] = run_base + lane_arena + 8u * (unsigned)i * rb;
+                return;
+            }
+        }
         const unsigned ad = slot + 8u * (unsigned)(lane >> 4);
         u32x2 m0 = lds_b64<0>(ad), m1 = lds_b64<32>(ad), m2 = lds_b64<64>(ad), m3 = lds_b64<96>(ad);
         lgkm_wait_tr(m0, m1, m2, m3);
@@ -563,17 +580,6 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_bf16_kernel(AttnArgs a) 
             mdec[i] = (ld_row0 + 4 * i < valid_rows && mw[i][1] == 0u && mw[i][0] <= max_arena_row)
                           ? 2u * mw[i][0] * rb
                           : ~0u;
-        // a run: row 4i + lane/16 of the group at run_base + that row's offset
-        // (lane 0 holds row 0; an unmapped row never matches, ~0u being odd
-        // and every arena offset even)
-        if constexpr (kRuns) {
-            run_base = (unsigned)__builtin_amdgcn_readfirstlane((int)mdec[0]);
-            bool ok = run_base != ~0u;
-#pragma unroll
-            for (int i = 0; i < 4; ++i)
-                ok = ok && mdec[i] == run_base + lane_arena + 8u * (unsigned)i * rb;
-            grp_run = __builtin_amdgcn_ballot_w64(!ok) == 0;
-        }
     };
     auto load_map = [&](int t) {
         if constexpr (!kMap) return;
