@@ -433,8 +433,6 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_bf16_kernel(AttnArgs a) 
     // KVMap words of a tile: 2 tile slots x 4 waves x 256 bytes; each wave
     // copies and reads only its own 256 bytes.
     __shared__ __attribute__((aligned(256))) unsigned char m_lds[2 * 4 * 256];
-    // Per-wave 2 KiB sink for copies whose data is not needed (KVMap kernel).
-    __shared__ __attribute__((aligned(1024))) unsigned char sink_lds[kMap ? 4 * 2048 : 16];
 
     const WgCoord c = decode_wg(a);
     if (!c.valid) return;  // whole workgroup: past the end of the layer order
@@ -543,17 +541,15 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_bf16_kernel(AttnArgs a) 
         if constexpr (!kMap) return;
         const unsigned slot = m_wave + 1024u * (unsigned)(t & 1);
         const long left = kend - (kbeg + (long)t * kBf16BlockKeys);
-        const int valid_rows = left < kBf16BlockKeys ? (int)left : kBf16BlockKeys;
         // rows at or past the range end are zero-filled padding, not entries
+        // (a tile past the end has none: valid_rows <= 0)
+        const int valid_rows = left < kBf16BlockKeys ? (int)left : kBf16BlockKeys;
         lgkm_wait1(hw);
         grp_mapped = __builtin_amdgcn_ballot_w64(lane < 32 && (lane & 1) && hw == 0u &&
                                                  16 * wave + (lane >> 1) < valid_rows) != 0;
         grp_run = false;
-        if (!grp_mapped) {
-#pragma unroll
-            for (int i = 0; i < 4; ++i) mdec[i] = ~0u;
-            return;
-        }
+        // mdec is read only by the copies of a mixed group (mapped, not a run)
+        if (__builtin_expect(!grp_mapped, 1)) return;
         if constexpr (kRuns) {
             // Lanes 0-31 already hold the group's 16 entries (entry e: low
             // word in lane 2e, high word in lane 2e+1). A run: all 16 rows
@@ -585,7 +581,8 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_bf16_kernel(AttnArgs a) 
         if constexpr (!kMap) return;
         const long t0 = kbeg + (long)t * kBf16BlockKeys;
         const long left = kend - t0;
-        const int nrec = (int)((left < kBf16BlockKeys ? left : kBf16BlockKeys) * 8);
+        // tiles past the range end (the loop prefetches two ahead) read zeros
+        const int nrec = left <= 0 ? 0 : (int)((left < kBf16BlockKeys ? left : kBf16BlockKeys) * 8);
         const __amdgpu_buffer_rsrc_t mrs = __builtin_amdgcn_make_buffer_rsrc(
             const_cast<long*>(map + t0), (short)0, nrec, kBufFlags);
         KVP_LDS void* md = (KVP_LDS void*)(uintptr_t)(
@@ -646,23 +643,16 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_bf16_kernel(AttnArgs a) 
     };
     // The copies interleaved with the QK MFMAs: the map-free kernel's copies
     // (no per-lane source choice, no branch between the MFMAs), from the
-    // arena for a run. For a group mixing arena and original rows, whose
-    // copies were issued before the tile (copy_pair), they land in the wave's
-    // sink instead (scalar select of the LDS target and the descriptor).
-    const unsigned sink = (unsigned)(uintptr_t)sink_lds + 2048u * (unsigned)wave;
-    // A sinked copy goes through a descriptor of zero records: it reads
-    // nothing from memory (out-of-range loads return zeros).
-    const __amdgpu_buffer_rsrc_t empty_rs =
-        __builtin_amdgcn_make_buffer_rsrc(const_cast<unsigned char*>(Kb), (short)0, 0, kBufFlags);
+    // arena for a run. A group mixing arena and original rows takes them too
+    // (original rows) and overwrites them after the tile's MFMAs with
+    // copy_pair's per-lane sources, once they have landed.
     auto copy_plain = [&](int i) {
-        const bool to_sink = kMap && grp_mapped && !(kRuns && grp_run);
-        KVP_LDS void* kd = (KVP_LDS void*)(uintptr_t)(to_sink ? sink : koff + 1024u * i);
-        KVP_LDS void* vd = (KVP_LDS void*)(uintptr_t)(to_sink ? sink + 1024u : voff + 1024u * i);
-        const __amdgpu_buffer_rsrc_t ks = to_sink ? empty_rs : krs;
-        const __amdgpu_buffer_rsrc_t vs = to_sink ? empty_rs : vrs;
+        KVP_LDS void* kd = (KVP_LDS void*)(uintptr_t)(koff + 1024u * i);
+        KVP_LDS void* vd = (KVP_LDS void*)(uintptr_t)(voff + 1024u * i);
         const unsigned step = (unsigned)i * cp_step;
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(ks, kd, 16, cp_k + step + kofs[i], 0, 0, kColdAux);
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(vs, vd, 16, cp_v + step + vofs, 0, 0, kColdAux);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(krs, kd, 16, cp_k + step + kofs[i], 0, 0,
+                                                 kColdAux);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(vrs, vd, 16, cp_v + step + vofs, 0, 0, kColdAux);
     };
 
     f32x16 o[4];
@@ -856,7 +846,7 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_bf16_kernel(AttnArgs a) 
         wait_vm<0>();
         read_check(0);
         decode_map(0);
-        if (ntiles > 1) load_map(1);
+        load_map(1);
         prep_tile(0, k_lds0, v_lds0);
 #pragma unroll
         for (int i = 0; i < 4; ++i) copy_pair(i);
@@ -864,7 +854,7 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_bf16_kernel(AttnArgs a) 
     // Compiler-visible wait for every load so far (Q, map, tile 0): the loop
     // then never waits for vector memory on the Q registers' account.
     __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
-    if (ntiles > 1) read_check(1);
+    if (ntiles > 0) read_check(1);
     for (int t = 0; t < ntiles; ++t) {
         // tile t lives in stage t & 1; tile t+1 streams into the other stage,
         // which every wave finished reading before the barrier that closed
@@ -873,41 +863,43 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_bf16_kernel(AttnArgs a) 
         unsigned char* vcur = (t & 1) ? v_lds1 : v_lds0;
         unsigned char* knext = (t & 1) ? k_lds0 : k_lds1;
         unsigned char* vnext = (t & 1) ? v_lds0 : v_lds1;
-        const bool more = t + 1 < ntiles;
         // each wave's copies of tile t (and map copies) have landed, then
         // the barrier publishes the whole tile
         wait_vm<0>();
         wg_barrier();
-        // The copies for tile t+1 are issued unconditionally, so the QK
-        // k-steps they sit between stay one basic block: past the last tile
-        // the descriptors cover no rows (every row reads as zeros) and no
-        // KVMap words are decoded (every row takes the original K/V path).
-        if (more) {
-            decode_map(t + 1);
-            if (kMap && t + 2 < ntiles) load_map(t + 2);
-        } else if (kMap) {
-            grp_mapped = false;
-            grp_run = false;
-#pragma unroll
-            for (int i = 0; i < 4; ++i) mdec[i] = ~0u;
-        }
+        // The copies for tile t+1 and the map copy for tile t+2 are issued
+        // unconditionally, so the QK k-steps they sit between stay one basic
+        // block: past the last tile the descriptors cover no rows (every row
+        // and map word reads as zero) and no KVMap entry is decoded (rows past
+        // the range end are not entries).
+        decode_map(t + 1);
+        load_map(t + 2);
         prep_tile(t + 1, knext, vnext);
-        if (!active || (kMap && grp_mapped && !(kRuns && grp_run))) {
-            // inactive waves, and groups mixing arena and original rows
-            // (wave-uniform): each row's source chosen per lane, copies
-            // issued before the tile's MFMAs
-#pragma unroll
-            for (int i = 0; i < 4; ++i) copy_pair(i);
-        }
+        // wave-uniform: the group mixes arena and original rows, each row's
+        // source chosen per lane (copy_pair)
+        const bool mixed = kMap && grp_mapped && !(kRuns && grp_run);
         if (active) {
             compute_tile(t, kcur, vcur, [&](int ks) {
                 if ((ks & 1) == 0) copy_plain(ks >> 1);
             });
+            if (__builtin_expect(mixed, 0)) {
+                // the plain copies (original rows) land first, then the
+                // per-lane copies overwrite the same LDS rows
+                wait_vm<0>();
+#pragma unroll
+                for (int i = 0; i < 4; ++i) copy_pair(i);
+            }
+        } else if (mixed) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) copy_pair(i);
+        } else {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) copy_plain(i);
         }
-        if (kMap && t + 2 < ntiles) {
-            // the map copy of tile t+2 was issued before this iteration's 8
-            // (or, for a group with arena rows, 16) tile copies: once at most
-            // 8 loads are outstanding it has landed
+        if constexpr (kMap) {
+            // the map copy of tile t+2 was issued before this iteration's
+            // tile copies and (mixed group) waited for with them, so once at
+            // most 8 loads are outstanding it has landed
             wait_vm<8>();
             read_check(t + 2);
         }
