@@ -455,10 +455,11 @@ void plan_frame_layer(Pipeline& p, KVTileManager& mgr, int f, const char* k, con
 
 // Copy of c K/V rows from row `row` to physical rows [phys, phys + c),
 // appended to the run table: runs of consecutive rows (also across tiles)
-// of at most ~24 KiB each.
+// of at most ~12 KiB each, which one workgroup of the staging kernel moves
+// in a single pass of loads (one round trip to memory per run).
 void layer_add_copy(Pipeline& p, long row, long phys, long c) {
     const long row_bytes = 2L * p.D * p.elem;
-    const long per_run = std::max<long>(1, std::min<long>(kvp::kLayerCopyRows, 24576 / row_bytes));
+    const long per_run = std::max<long>(1, std::min<long>(kvp::kLayerCopyRows, 12288 / row_bytes));
     while (c > 0) {
         if (!p.layer_copies.empty()) {
             kvp::LayerCopyRun& r = p.layer_copies.back();
