@@ -62,8 +62,6 @@ constexpr float kLog2e = 1.4426950408889634f;
 
 constexpr int kBf16BlockKeys = 64;
 constexpr int kF32BlockKeys = 32;
-constexpr int kF32RowPad = 4;  // floats of padding per LDS row (fp32 path)
-constexpr int kF32LdsRow = kHeadDim + kF32RowPad;
 
 struct AttnArgs {
     const void* q;
@@ -337,6 +335,21 @@ __device__ __forceinline__ void lgkm_wait2(u32x4& a, u32x4& b) {
 // issue order and no scalar-memory load is issued in the compute phase).
 __device__ __forceinline__ void lgkm_wait2_keep2(u32x4& a, u32x4& b) {
     asm volatile("s_waitcnt lgkmcnt(2)" : "+v"(a), "+v"(b)::"memory");
+}
+
+// fp32 kernel: wait for all but the newest LDS read / for all of them.
+__device__ __forceinline__ void lgkm_wait_keep1(u32x4& a) {
+    asm volatile("s_waitcnt lgkmcnt(1)" : "+v"(a)::"memory");
+}
+__device__ __forceinline__ void lgkm_wait1x4(u32x4& a) {
+    asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(a)::"memory");
+}
+// fp32 kernel: wait for every LDS read, the 16 values of a V block among them.
+__device__ __forceinline__ void lgkm_wait16(unsigned (&d)[16]) {
+    asm volatile("s_waitcnt lgkmcnt(0)"
+                 : "+v"(d[0]), "+v"(d[1]), "+v"(d[2]), "+v"(d[3]), "+v"(d[4]), "+v"(d[5]),
+                   "+v"(d[6]), "+v"(d[7]), "+v"(d[8]), "+v"(d[9]), "+v"(d[10]), "+v"(d[11]),
+                   "+v"(d[12]), "+v"(d[13]), "+v"(d[14]), "+v"(d[15])::"memory");
 }
 
 // Waits until at most N LDS reads are outstanding.
@@ -922,38 +935,62 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_bf16_kernel(AttnArgs a) 
 
 // ---------------------------------------------------------------------------
 // fp32 kernel
+//
+// Same decomposition as the bf16 kernel (4 waves x 32 queries per
+// workgroup), v_mfma_f32_32x32x2_f32, 32-key tiles. K and V tiles (32 keys x
+// 128 dims, 16 KiB each) stream global -> LDS with buffer_load_dwordx4 ...
+// lds into a two-stage ring; the copies of tile t+1 go out between the QK
+// MFMAs of tile t. An LDS row is one key's 512 bytes (32 chunks of 16 B):
+//   K: physical chunk = logical ^ (row & 15): the ds_read_b128 of 32 rows x
+//      one chunk is conflict free;
+//   V: physical chunk = logical ^ 8*((row >> 2) & 1): the ds_read_b32 of
+//      rows r and r+4 x 32 columns lands on all 64 banks once.
+// Copy i (0..3) of wave w fills bytes [(4w+i) KiB, +1 KiB) of a K (and a V)
+// stage: rows 8w + 2i + lane/32, physical chunk lane % 32. Rows past the
+// range end read zeros through the tile's buffer descriptor. With a KVMap,
+// a row whose entry m >= 0 is copied from arena row m instead, through a
+// 64-bit address per lane; the entries of tile t+2 are loaded into
+// registers during tile t.
+// Softmax as in the bf16 kernel: exponentials against the running max, the
+// max raised (and O, l rescaled) only when a tile's row sum exceeds 2^64 or
+// is not finite; P stays fp32.
 // ---------------------------------------------------------------------------
 
-constexpr int kF32TileFloats = kF32BlockKeys * kF32LdsRow;
+constexpr int kF32TileBytes = kF32BlockKeys * kHeadDim * 4;  // 16 KiB
 
+template <bool kMap>
 __global__ __launch_bounds__(kThreads, 2) void attn_fwd_f32_kernel(AttnArgs a) {
-    __shared__ __attribute__((aligned(16))) float lds[2 * kF32TileFloats];
-    float* ks_lds = lds;
-    float* vs_lds = lds + kF32TileFloats;
+    __shared__ __attribute__((aligned(1024))) unsigned char k_lds0[kF32TileBytes];
+    __shared__ __attribute__((aligned(1024))) unsigned char v_lds0[kF32TileBytes];
+    __shared__ __attribute__((aligned(1024))) unsigned char k_lds1[kF32TileBytes];
+    __shared__ __attribute__((aligned(1024))) unsigned char v_lds1[kF32TileBytes];
 
     const WgCoord c = decode_wg(a);
     if (!c.valid) return;  // whole workgroup: past the end of the layer order
     const int tid = threadIdx.x;
-    const int wave = tid >> 6;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int lane = tid & 63;
     const int lq = lane & 31;
     const int hh = lane >> 5;
-    // waves with no valid query load their share of each tile, skip the MFMAs
+    // waves with no valid query issue their share of each tile's copies and
+    // skip the MFMAs
     const bool active = c.qb * kBlockQ + wave * 32 < a.nq;
 
     long kbeg, kend;
     wg_keys(a, c, kbeg, kend);
+    const int ntiles = (int)((kend - kbeg + kF32BlockKeys - 1) / kF32BlockKeys);
 
     const float* Q = reinterpret_cast<const float*>(a.q) + (long)c.frame * a.q_fstride;
-    const float* K = reinterpret_cast<const float*>(a.k) + (long)c.frame * a.kv_fstride;
-    const float* V = reinterpret_cast<const float*>(a.v) + (long)c.frame * a.kv_fstride;
-    const float* A = a.arena ? reinterpret_cast<const float*>(
-                                   reinterpret_cast<const unsigned char*>(a.arena) +
-                                   (long)c.frame * a.arena_fstride)
-                             : nullptr;
-    const long* map = a.kvmap ? a.kvmap + (long)c.frame * a.map_fstride : nullptr;
-    const int hoff = c.head * kHeadDim;
+    const unsigned char* Kb = reinterpret_cast<const unsigned char*>(a.k) + 4L * c.frame * a.kv_fstride;
+    const unsigned char* Vb = reinterpret_cast<const unsigned char*>(a.v) + 4L * c.frame * a.kv_fstride;
+    const unsigned char* Ab =
+        kMap ? reinterpret_cast<const unsigned char*>(a.arena) + (long)c.frame * a.arena_fstride
+             : nullptr;
+    const long* map = kMap ? a.kvmap + (long)c.frame * a.map_fstride : nullptr;
     const long D = a.D;
+    const long row_bytes = 4L * D;
+    const unsigned rb = (unsigned)row_bytes;
+    const long hoff_b = 4L * c.head * kHeadDim;
 
     // Query fragment: lane holds Q[q][8*j + 4*hh .. +4) for j = 0..15;
     // MFMA k-step (j, i) pairs head dim 8*j + 4*hh + i of both operands.
@@ -961,38 +998,55 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_f32_kernel(AttnArgs a) {
     const int qc = q < a.nq ? q : a.nq - 1;
     f32x4 qf[16];
     {
-        const float* qp = Q + (long)qc * D + hoff + 4 * hh;
+        const float* qp = Q + (long)qc * D + c.head * kHeadDim + 4 * hh;
 #pragma unroll
         for (int j = 0; j < 16; ++j) qf[j] = *reinterpret_cast<const f32x4*>(qp + 8 * j);
     }
 
-    // Staging: 16-byte chunk ch (4 floats) of the head slice, keys grp + 8*i.
-    const int ld_ch = tid & 31;
-    const int ld_grp = tid >> 5;
-
-    f32x4 kr[4], vr[4];
-    auto load_tile = [&](long t0) {
+    // Copy geometry: copy i of this lane moves tile row 8w + 2i + lane/32,
+    // physical chunk lane % 32.
+    const int pch = lane & 31;
+    auto cp_row = [&](int i) { return 8 * wave + 2 * i + (lane >> 5); };
+    auto k_chunk = [&](int i) { return pch ^ (cp_row(i) & 15); };
+    auto v_chunk = [&](int i) { return pch ^ (((cp_row(i) >> 2) & 1) << 3); };
+    auto desc = [&](const unsigned char* base, int t) {
+        const long t0 = kbeg + (long)t * kF32BlockKeys;
+        const long left = kend - t0;
+        // tiles at or past the end (the loop's trailing copies) cover no rows
+        const long rows = left <= 0 ? 0 : (left < kF32BlockKeys ? left : kF32BlockKeys);
+        return __builtin_amdgcn_make_buffer_rsrc(const_cast<unsigned char*>(base + t0 * row_bytes),
+                                                 (short)0, (int)(rows * row_bytes), kBufFlags);
+    };
+    // KVMap entries of this lane's 4 copy rows of tile t (-1 past the end)
+    auto load_entries = [&](int t, long (&m)[4]) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            const long j = t0 + ld_grp + 8 * i;
-            if (j < kend) {
-                const long m = map ? map[j] : -1L;
-                const float* kp = m >= 0 ? A + m * 2 * D + hoff : K + j * D + hoff;
-                const float* vp = m >= 0 ? A + m * 2 * D + D + hoff : V + j * D + hoff;
-                kr[i] = *reinterpret_cast<const f32x4*>(kp + 4 * ld_ch);
-                vr[i] = *reinterpret_cast<const f32x4*>(vp + 4 * ld_ch);
-            } else {
-                kr[i] = f32x4{0.f, 0.f, 0.f, 0.f};
-                vr[i] = f32x4{0.f, 0.f, 0.f, 0.f};
-            }
+            const long j = kbeg + (long)t * kF32BlockKeys + cp_row(i);
+            m[i] = j < kend ? map[j] : -1L;
         }
     };
-    auto store_tile = [&]() {
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int row = ld_grp + 8 * i;
-            *reinterpret_cast<f32x4*>(ks_lds + row * kF32LdsRow + 4 * ld_ch) = kr[i];
-            *reinterpret_cast<f32x4*>(vs_lds + row * kF32LdsRow + 4 * ld_ch) = vr[i];
+    long mcur[4] = {-1L, -1L, -1L, -1L};
+    long mnext[4] = {-1L, -1L, -1L, -1L};
+    __amdgpu_buffer_rsrc_t krs, vrs;
+    unsigned kdst = 0, vdst = 0;
+    auto prep_tile = [&](int t, unsigned char* kd, unsigned char* vd) {
+        krs = desc(Kb, t);
+        vrs = desc(Vb, t);
+        kdst = (unsigned)__builtin_amdgcn_readfirstlane((int)(uintptr_t)kd) + 4096u * wave;
+        vdst = (unsigned)__builtin_amdgcn_readfirstlane((int)(uintptr_t)vd) + 4096u * wave;
+    };
+    auto copy = [&](int i) {
+        KVP_LDS void* kd = (KVP_LDS void*)(uintptr_t)(kdst + 1024u * i);
+        KVP_LDS void* vd = (KVP_LDS void*)(uintptr_t)(vdst + 1024u * i);
+        const int kc = k_chunk(i), vc = v_chunk(i);
+        if (kMap && mcur[i] >= 0) {
+            const unsigned char* ar = Ab + mcur[i] * 2 * row_bytes + hoff_b;
+            __builtin_amdgcn_global_load_lds(ar + 16 * kc, kd, 16, 0, 0);
+            __builtin_amdgcn_global_load_lds(ar + row_bytes + 16 * vc, vd, 16, 0, 0);
+        } else {
+            const unsigned ro = (unsigned)cp_row(i) * rb + (unsigned)hoff_b;
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(krs, kd, 16, ro + 16u * kc, 0, 0, 0);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(vrs, vd, 16, ro + 16u * vc, 0, 0, 0);
         }
     };
 
@@ -1003,56 +1057,148 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_f32_kernel(AttnArgs a) {
         for (int v = 0; v < 16; ++v) o[nb][v] = 0.f;
     float m_run = -INFINITY;
     float l_run = 0.f;
+    const float cl2 = a.scale_log2;
+    const unsigned kswz = (unsigned)(lq & 15);
 
-    long t0 = kbeg;
-    if (t0 < kend) load_tile(t0);
-    for (; t0 < kend; t0 += kF32BlockKeys) {
-        store_tile();
+    if (ntiles > 0) {
+        if constexpr (kMap) {
+            load_entries(0, mcur);
+            load_entries(1, mnext);
+        }
+        prep_tile(0, k_lds0, v_lds0);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) copy(i);
+    }
+    for (int t = 0; t < ntiles; ++t) {
+        unsigned char* kcur = (t & 1) ? k_lds1 : k_lds0;
+        unsigned char* vcur = (t & 1) ? v_lds1 : v_lds0;
+        // every copy of tile t (and the entries of tile t+1) has landed; the
+        // barrier publishes the tile and closes the reads of the other stage
+        __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
         __syncthreads();
-        if (t0 + kF32BlockKeys < kend) load_tile(t0 + kF32BlockKeys);
+        if constexpr (kMap) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) mcur[i] = mnext[i];
+            load_entries(t + 2, mnext);
+        }
+        prep_tile(t + 1, (t & 1) ? k_lds0 : k_lds1, (t & 1) ? v_lds0 : v_lds1);
         if (!active) {
-            __syncthreads();
+#pragma unroll
+            for (int i = 0; i < 4; ++i) copy(i);
             continue;
         }
 
+        // S^T = K Q^T: 16 ds_read_b128 of K (row lq, logical chunk 2j + hh),
+        // each read two k-steps ahead of its 4 MFMAs
+        const unsigned kbase = (unsigned)(uintptr_t)kcur + (unsigned)(lq * 512);
+        auto kaddr = [&](int j) {
+            return kbase + 256u * (unsigned)(j >> 3) +
+                   ((((unsigned)(2 * (j & 7) + hh)) ^ kswz) << 4);
+        };
         f32x16 st;
 #pragma unroll
         for (int v = 0; v < 16; ++v) st[v] = 0.f;
+        u32x4 kr[3];
+        kr[0] = lds_b128<0>(kaddr(0));
+        kr[1] = lds_b128<0>(kaddr(1));
 #pragma unroll
         for (int j = 0; j < 16; ++j) {
-            const f32x4 ka = *reinterpret_cast<const f32x4*>(ks_lds + lq * kF32LdsRow + 8 * j + 4 * hh);
+            u32x4& ka = kr[j % 3];
+            if (j + 1 < 16)
+                lgkm_wait_keep1(ka);
+            else
+                lgkm_wait1x4(ka);
+            if (j + 2 < 16) kr[(j + 2) % 3] = lds_b128<0>(kaddr(j + 2));
+            const f32x4 kf = __builtin_bit_cast(f32x4, ka);
 #pragma unroll
             for (int i = 0; i < 4; ++i)
-                st = __builtin_amdgcn_mfma_f32_32x32x2f32(ka[i], qf[j][i], st, 0, 0, 0);
+                st = __builtin_amdgcn_mfma_f32_32x32x2f32(kf[i], qf[j][i], st, 0, 0, 0);
+            if ((j & 3) == 3) copy(j >> 2);
         }
 
         float s[16];
 #pragma unroll
         for (int v = 0; v < 16; ++v) s[v] = st[v];
+        const long t0 = kbeg + (long)t * kF32BlockKeys;
         if (t0 + kF32BlockKeys > kend) {
-            const long lim = kend - t0;
+            const int lim = (int)(kend - t0) - 4 * hh;
 #pragma unroll
             for (int v = 0; v < 16; ++v) {
-                const int key = 8 * (v >> 2) + 4 * hh + (v & 3);
-                if (key >= lim) s[v] = -INFINITY;
+                const int kc = 8 * (v >> 2) + (v & 3);
+                if (kc >= lim) s[v] = -INFINITY;
             }
         }
-        const float corr = softmax_update<16>(s, a.scale_log2, m_run, l_run);
+        float p[16];
+        auto exp_tile = [&](float mref) {
+            float ra = 0.f, rb2 = 0.f;
+#pragma unroll
+            for (int v = 0; v < 16; v += 2) {
+                p[v] = fast_exp2(fmaf(s[v], cl2, -mref));
+                p[v + 1] = fast_exp2(fmaf(s[v + 1], cl2, -mref));
+                ra += p[v];
+                rb2 += p[v + 1];
+            }
+            const float rs = ra + rb2;
+            return rs + other_half(rs);
+        };
+        float tot = exp_tile(m_run);
+        if (__builtin_amdgcn_ballot_w64(!(tot <= kRowSumLimit))) {
+            float mx = s[0];
+#pragma unroll
+            for (int v = 1; v < 16; ++v) mx = fmaxf(mx, s[v]);
+            mx = fmaxf(mx, other_half(mx));
+            const float m_new = fmaxf(m_run, mx * cl2);
+            const float corr = fast_exp2(m_run - m_new);  // 0 while m_run is -inf
+            l_run *= corr;
+#pragma unroll
+            for (int nb = 0; nb < 4; ++nb)
+#pragma unroll
+                for (int v = 0; v < 16; ++v) o[nb][v] *= corr;
+            m_run = m_new;
+            tot = exp_tile(m_run);
+        }
+        l_run += tot;
 
+        // O^T += V^T P^T: lane reads V[key][32 nb + lq] for its keys
+        // 4*hh + 8*(v/4) + v%4 (row offsets are immediates); the V swizzle
+        // bit of those rows is hh. A block's 16 reads go out while the
+        // previous block's MFMAs run.
+        const unsigned vbase = (unsigned)(uintptr_t)vcur + (unsigned)(4 * hh * 512 + 4 * (lq & 3));
+        auto read_vb = [&](unsigned (&d)[16], int nb) {
+            const unsigned ad = vbase + 16u * (unsigned)((8 * nb + (lq >> 2)) ^ (8 * hh));
+            d[0] = lds_b32<0 * 512>(ad);
+            d[1] = lds_b32<1 * 512>(ad);
+            d[2] = lds_b32<2 * 512>(ad);
+            d[3] = lds_b32<3 * 512>(ad);
+            d[4] = lds_b32<8 * 512>(ad);
+            d[5] = lds_b32<9 * 512>(ad);
+            d[6] = lds_b32<10 * 512>(ad);
+            d[7] = lds_b32<11 * 512>(ad);
+            d[8] = lds_b32<16 * 512>(ad);
+            d[9] = lds_b32<17 * 512>(ad);
+            d[10] = lds_b32<18 * 512>(ad);
+            d[11] = lds_b32<19 * 512>(ad);
+            d[12] = lds_b32<24 * 512>(ad);
+            d[13] = lds_b32<25 * 512>(ad);
+            d[14] = lds_b32<26 * 512>(ad);
+            d[15] = lds_b32<27 * 512>(ad);
+        };
+        unsigned vv[2][16];
+        read_vb(vv[0], 0);
 #pragma unroll
         for (int nb = 0; nb < 4; ++nb) {
+            unsigned (&cur)[16] = vv[nb & 1];
+            lgkm_wait16(cur);
+            if (nb < 3) read_vb(vv[(nb + 1) & 1], nb + 1);
 #pragma unroll
-            for (int v = 0; v < 16; ++v) o[nb][v] *= corr;
-#pragma unroll
-            for (int v = 0; v < 16; ++v) {
-                const int key = 8 * (v >> 2) + 4 * hh + (v & 3);
-                const float va = vs_lds[key * kF32LdsRow + 32 * nb + lq];
-                o[nb] = __builtin_amdgcn_mfma_f32_32x32x2f32(va, s[v], o[nb], 0, 0, 0);
-            }
+            for (int v = 0; v < 16; ++v)
+                o[nb] = __builtin_amdgcn_mfma_f32_32x32x2f32(__uint_as_float(cur[v]), p[v], o[nb],
+                                                              0, 0, 0);
         }
-        __syncthreads();
     }
-
+    // the trailing copies land before the workgroup's LDS is released
+    __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
+    if (!active) return;
     store_rows_f32(a, c, q, hh, o, m_run, l_run);
 }
 
@@ -1203,7 +1349,7 @@ DeviceInfo device_info(int dev) {
             di.wg_per_cu_bf16 = nb;
         nb = 0;
         if (hipOccupancyMaxActiveBlocksPerMultiprocessor(
-                &nb, attn_fwd_f32_kernel, kThreads, 0) == hipSuccess && nb > 0)
+                &nb, attn_fwd_f32_kernel<true>, kThreads, 0) == hipSuccess && nb > 0)
             di.wg_per_cu_f32 = nb;
         di.ok = true;
     }
@@ -1499,7 +1645,12 @@ int launch_attention(const AttnLaunch& L) {
             hipLaunchKernelGGL((attn_fwd_bf16_kernel<__bf16, false, false>),
                                dim3((unsigned)p.grid), dim3(kThreads), 0, st, a);
     } else {
-        hipLaunchKernelGGL(attn_fwd_f32_kernel, dim3((unsigned)p.grid), dim3(kThreads), 0, st, a);
+        if (a.kvmap)
+            hipLaunchKernelGGL(attn_fwd_f32_kernel<true>, dim3((unsigned)p.grid), dim3(kThreads), 0,
+                               st, a);
+        else
+            hipLaunchKernelGGL(attn_fwd_f32_kernel<false>, dim3((unsigned)p.grid), dim3(kThreads), 0,
+                               st, a);
     }
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) {
