@@ -27,7 +27,8 @@
 // bf16 path: v_mfma_f32_32x32x16_bf16; K tile [64][128] row-major and V tile
 // transposed to [128][64] in LDS (16-byte chunks XOR-swizzled against bank
 // conflicts); P is rounded to bf16 for the PV product.
-// fp32 path: v_mfma_f32_32x32x2_f32; K and V tiles [32][128(+4 pad)] fp32.
+// fp32 path: v_mfma_f32_32x32x2_f32; K and V tiles [32][128] fp32, 16-byte
+// chunks XOR-swizzled in LDS, P kept in fp32.
 //
 // Invalid query rows (q >= nq) are clamped for loads and never stored; all
 // threads reach every barrier. Invalid key rows of the last tile are zero in
