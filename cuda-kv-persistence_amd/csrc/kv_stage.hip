@@ -20,9 +20,10 @@
 // the launch that read it has completed.
 //
 // Layer staging (the frame pipeline's whole-layer run) has its own kernel:
-// run tables of up to ~24 KiB row copies and up to 1024-entry map runs, one
-// workgroup per run, read from the same ring; every thread moves 16-byte
-// chunks with four loads in flight.
+// run tables of row copies (the frame pipeline sizes them to ~12 KiB, one
+// pass of loads per workgroup) and up to 1024-entry map runs, one workgroup
+// per run, read from the same ring; every thread moves 16-byte chunks with
+// up to four loads in flight.
 
 #include <hip/hip_runtime.h>
 
