@@ -130,6 +130,31 @@ def cpu_threads():
     return max(1, n)
 
 
+def mfma_ceiling():
+    """Dense bf16 rate the matrix cores sustain on this board when they do
+    nothing else (lib/libkvpprobe.so: two 256-thread workgroups per CU, four
+    independent v_mfma_f32_32x32x16_bf16 chains per wave on pseudo-random
+    operands, median of 5 launches of ~20 ms after a warm-up launch): the
+    power-limited counterpart of the published peak. None when the probe
+    library is not built."""
+    import ctypes
+    path = ROOT / "cuda-kv-persistence_amd" / "lib" / "libkvpprobe.so"
+    if not path.exists():
+        return None
+    lib = ctypes.CDLL(str(path))
+    fn = lib.kvpprobe_mfma_bf16
+    fn.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.POINTER(ctypes.c_double),
+                   ctypes.POINTER(ctypes.c_double)]
+    fn.restype = ctypes.c_int
+    tf, ms = ctypes.c_double(), ctypes.c_double()
+    if fn(150000, 5, ctypes.byref(tf), ctypes.byref(ms)) != 0:
+        raise RuntimeError("MFMA ceiling probe failed")
+    return {"tflops": round(tf.value, 1), "frac_of_peak": round(tf.value / BF16_PEAK_TFLOPS, 4),
+            "launch_ms": round(ms.value, 3),
+            "kernel": "v_mfma_f32_32x32x16_bf16 only on pseudo-random bf16 operands, "
+                      "2 workgroups x 4 waves per CU, 4 chains per wave"}
+
+
 def cpu_baseline(cfg, units_target: int):
     """Oracle fp32 attention (reference golden restated) on host cores."""
     import numpy as np
@@ -835,6 +860,11 @@ def main():
             torch.cuda.empty_cache()
             log(f"leg {name}: {t / c.frames:.4f} ms/frame, {tfl:.0f} TFLOP/s")
 
+    ceiling = mfma_ceiling()
+    if ceiling:
+        log(f"matrix-core ceiling {ceiling['tflops']} TFLOP/s "
+            f"({ceiling['frac_of_peak']:.3f} of the published peak)")
+
     cpu = None
     if not args.no_cpu_baseline:
         log("cpu baseline ...")
@@ -891,6 +921,8 @@ def main():
             "avg_launch_ms": lay_ms,
             "compulsory_read_bytes_per_launch": round(comp_frame * F),
             "compulsory_write_bytes_per_launch": round(F * cfg.tokens * 1536 * 2),
+            "mfma_ceiling": ceiling,
+            "frac_of_ceiling": (round(achieved / ceiling["tflops"], 4) if ceiling else None),
         },
         "cpu_baseline": cpu,
         "policies": policies,
