@@ -257,6 +257,10 @@ constexpr int kBufFlags = 0x00020000;
 // bf16/fp32 comfortably and O, l accumulate without rescaling.
 constexpr float kRowSumLimit = 18446744073709551616.0f;
 constexpr unsigned kVSwzTable = 0xAC60u;  // nibbles {0, 6, 12, 10}
+// Buffer offset past the records of every bf16 tile descriptor (a tile
+// covers at most 64 rows of 2*D bytes): a load there reads no memory and
+// returns zeros.
+constexpr unsigned kNoRecord = 0x80000000u;
 
 typedef __attribute__((ext_vector_type(4))) short v4i16;
 typedef __attribute__((ext_vector_type(2))) __bf16 bf16x2;
@@ -447,6 +451,10 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_bf16_kernel(AttnArgs a) 
     // KVMap words of a tile: 2 tile slots x 4 waves x 256 bytes; each wave
     // copies and reads only its own 256 bytes.
     __shared__ __attribute__((aligned(256))) unsigned char m_lds[2 * 4 * 256];
+    // Per-wave 2 KiB sink (KVMap kernel): the interleaved copies of a group
+    // mixing arena and original rows land there (reading nothing), while
+    // the group's own rows come from its per-lane copies.
+    __shared__ __attribute__((aligned(1024))) unsigned char sink_lds[kMap ? 4 * 2048 : 16];
 
     const WgCoord c = decode_wg(a);
     if (!c.valid) return;  // whole workgroup: past the end of the layer order
@@ -613,8 +621,11 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_bf16_kernel(AttnArgs a) 
     __amdgpu_buffer_rsrc_t krs, vrs;
     unsigned koff = 0, voff = 0;
     // copy_plain's per-lane offsets: copy i reads K at cp_k + i*cp_step +
-    // kofs[i] and V at cp_v + i*cp_step + vofs through krs / vrs
+    // kofs[i] and V at cp_v + i*cp_step + vofs through krs / vrs, into LDS
+    // bytes pk + i*pstep and pv + i*pstep
     unsigned cp_k = lane_row, cp_v = lane_row, cp_step = 4u * rb;
+    unsigned pk = 0, pv = 0, pstep = 1024u;
+    const unsigned sink = (unsigned)(uintptr_t)sink_lds + 2048u * (unsigned)wave;
     auto prep_tile = [&](int t, unsigned char* kdst, unsigned char* vdst) {
         const long t0 = kbeg + (long)t * kBf16BlockKeys;
         const long left = kend - t0;
@@ -630,6 +641,9 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_bf16_kernel(AttnArgs a) 
         cp_k = lane_row;
         cp_v = lane_row;
         cp_step = 4u * rb;
+        pk = koff;
+        pv = voff;
+        pstep = 1024u;
         if (kRuns && grp_run) {
             // [K row | V row] arena rows of the run: 2*rb apart, V rb after K
             krs = __builtin_amdgcn_make_buffer_rsrc(
@@ -638,6 +652,16 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_bf16_kernel(AttnArgs a) 
             cp_k = lane_arena;
             cp_v = lane_arena + rb;
             cp_step = 8u * rb;
+        } else if (kMap && grp_mapped) {
+            // a group mixing arena and original rows (copy_pair fills its
+            // rows): its plain copies aim past the tile's records, so they
+            // read nothing, and land in the wave's sink
+            cp_k = kNoRecord;
+            cp_v = kNoRecord;
+            cp_step = 0;
+            pk = sink;
+            pv = sink + 1024u;
+            pstep = 0;
         }
     };
     auto copy_pair = [&](int i) {
@@ -657,12 +681,12 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_bf16_kernel(AttnArgs a) 
     };
     // The copies interleaved with the QK MFMAs: the map-free kernel's copies
     // (no per-lane source choice, no branch between the MFMAs), from the
-    // arena for a run. A group mixing arena and original rows takes them too
-    // (original rows) and overwrites them after the tile's MFMAs with
-    // copy_pair's per-lane sources, once they have landed.
+    // arena for a run. A group mixing arena and original rows, whose rows
+    // copy_pair issued before the tile, sends them past the descriptor's
+    // records (no reads) into its sink.
     auto copy_plain = [&](int i) {
-        KVP_LDS void* kd = (KVP_LDS void*)(uintptr_t)(koff + 1024u * i);
-        KVP_LDS void* vd = (KVP_LDS void*)(uintptr_t)(voff + 1024u * i);
+        KVP_LDS void* kd = (KVP_LDS void*)(uintptr_t)(pk + pstep * (unsigned)i);
+        KVP_LDS void* vd = (KVP_LDS void*)(uintptr_t)(pv + pstep * (unsigned)i);
         const unsigned step = (unsigned)i * cp_step;
         __builtin_amdgcn_raw_ptr_buffer_load_lds(krs, kd, 16, cp_k + step + kofs[i], 0, 0,
                                                  kColdAux);
@@ -893,16 +917,13 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_bf16_kernel(AttnArgs a) 
         // source chosen per lane (copy_pair)
         const bool mixed = kMap && grp_mapped && !(kRuns && grp_run);
         if (active) {
-            compute_tile(t, kcur, vcur, [&](int ks) {
-                if ((ks & 1) == 0) copy_plain(ks >> 1);
-            });
             if (__builtin_expect(mixed, 0)) {
-                // the plain copies (original rows) land first, then the
-                // per-lane copies overwrite the same LDS rows
-                wait_vm<0>();
 #pragma unroll
                 for (int i = 0; i < 4; ++i) copy_pair(i);
             }
+            compute_tile(t, kcur, vcur, [&](int ks) {
+                if ((ks & 1) == 0) copy_plain(ks >> 1);
+            });
         } else if (mixed) {
 #pragma unroll
             for (int i = 0; i < 4; ++i) copy_pair(i);
@@ -912,8 +933,9 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_bf16_kernel(AttnArgs a) 
         }
         if constexpr (kMap) {
             // the map copy of tile t+2 was issued before this iteration's
-            // tile copies and (mixed group) waited for with them, so once at
-            // most 8 loads are outstanding it has landed
+            // tile copies (8, or 16 for a mixed group whose last 8 go to
+            // the sink), so once at most 8 loads are outstanding it has
+            // landed
             wait_vm<8>();
             read_check(t + 2);
         }
