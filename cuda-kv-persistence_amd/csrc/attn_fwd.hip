@@ -314,17 +314,6 @@ __device__ __forceinline__ unsigned lds_b32(unsigned addr) {
     return r;
 }
 
-__device__ __forceinline__ void lgkm_wait1(unsigned& a) {
-    asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(a)::"memory");
-}
-
-template <int OFF>
-__device__ __forceinline__ u32x2 lds_b64(unsigned addr) {
-    u32x2 r;
-    asm volatile("ds_read_b64 %0, %1 offset:%2" : "=v"(r) : "v"(addr), "n"(OFF) : "memory");
-    return r;
-}
-
 template <int OFF>
 __device__ __forceinline__ u32x2 lds_tr16(unsigned addr) {
     u32x2 r;
@@ -361,10 +350,6 @@ __device__ __forceinline__ void lgkm_wait16(unsigned (&d)[16]) {
 template <int N>
 __device__ __forceinline__ void lgkm_wait_tr_n(u32x2& a, u32x2& b, u32x2& c, u32x2& d) {
     asm volatile("s_waitcnt lgkmcnt(%4)" : "+v"(a), "+v"(b), "+v"(c), "+v"(d) : "n"(N) : "memory");
-}
-
-__device__ __forceinline__ void lgkm_wait_tr(u32x2& a, u32x2& b, u32x2& c, u32x2& d) {
-    asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(a), "+v"(b), "+v"(c), "+v"(d)::"memory");
 }
 
 // bf16 kernel epilogue: the wave's 32 query rows x 128 dims go out as
@@ -448,9 +433,6 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_bf16_kernel(AttnArgs a) 
     __shared__ __attribute__((aligned(1024))) unsigned char v_lds0[kBf16TileBytes];
     __shared__ __attribute__((aligned(1024))) unsigned char k_lds1[kBf16TileBytes];
     __shared__ __attribute__((aligned(1024))) unsigned char v_lds1[kBf16TileBytes];
-    // KVMap words of a tile: 2 tile slots x 4 waves x 256 bytes; each wave
-    // copies and reads only its own 256 bytes.
-    __shared__ __attribute__((aligned(256))) unsigned char m_lds[2 * 4 * 256];
     // Per-wave 2 KiB sink (KVMap kernel): the interleaved copies of a group
     // mixing arena and original rows land there (reading nothing), while
     // the group's own rows come from its per-lane copies.
@@ -469,7 +451,18 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_bf16_kernel(AttnArgs a) 
 
     long kbeg, kend;
     wg_keys(a, c, kbeg, kend);
-    const int ntiles = (int)((kend - kbeg + kBf16BlockKeys - 1) / kBf16BlockKeys);
+    // keys of the range (key indices stay below 2^31: checked at launch)
+    const int nkeys = (int)(kend - kbeg);
+    const int ntiles = (nkeys + kBf16BlockKeys - 1) / kBf16BlockKeys;
+    // Rows of tile t: 64 before the last tile, last_rows in it, none past
+    // it (the loop prefetches past the end). Written as a choice between
+    // loop-invariant values, so that it stays a scalar select (a clamp of
+    // nkeys - 64*t becomes a vector min/max here, and a descriptor built
+    // from a vector value is taken apart lane by lane).
+    const int last_rows = nkeys - (ntiles - 1) * kBf16BlockKeys;
+    auto tile_rows_x = [&](int t, int full, int last) {
+        return t < ntiles - 1 ? full : (t == ntiles - 1 ? last : 0);
+    };
 
     const __bf16* Q = reinterpret_cast<const __bf16*>(a.q) + (long)c.frame * a.q_fstride;
     const unsigned char* Kb = reinterpret_cast<const unsigned char*>(a.k) + 2L * c.frame * a.kv_fstride;
@@ -515,62 +508,50 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_bf16_kernel(AttnArgs a) 
     const __amdgpu_buffer_rsrc_t arena_rs =
         __builtin_amdgcn_make_buffer_rsrc(const_cast<unsigned char*>(Ab), (short)0, -1, kBufFlags);
 
-    // KVMap entries of a tile are copied into LDS two tiles ahead (one
-    // 4-byte copy per lane: wave w takes the tile's rows 16w.. as 32 words;
-    // lanes past the tile's end read zeros). Right before the tile's own K/V
-    // copies are issued they are decoded into arena byte offsets; by then
-    // the map copy has landed (the loop waits for all of a wave's copies at
-    // the top of each iteration). Arena rows are addressed with 32-bit byte
-    // offsets from the arena base: an entry m is used when its row ends
-    // within 4 GiB of that base (2*(m+1)*row_bytes <= 2^32); any negative
-    // entry, or one beyond that, reads the original K/V row (offset ~0u).
-    // Rows at or past the range end take the original-row path too, whose
-    // descriptor reads them as zeros (their map words are zero-filled
-    // padding, not entries).
-    const unsigned m_wave = (unsigned)(uintptr_t)m_lds + 256u * wave;
+    // KVMap entries of a tile are loaded into registers two tiles ahead (one
+    // 4-byte load per lane: lanes 0-31 of wave w hold the 32 words of the
+    // tile's rows 16w..16w+15, entry e's low word in lane 2e and its high
+    // word in lane 2e+1; words past the tile's end read as zeros). Right
+    // before the tile's own K/V copies are issued they are decoded into
+    // arena byte offsets; by then the load has landed (the loop waits for
+    // all of a wave's loads at the top of each iteration). Arena rows are
+    // addressed with 32-bit byte offsets from the arena base: an entry m is
+    // used when its row ends within 4 GiB of that base
+    // (2*(m+1)*row_bytes <= 2^32); any negative entry, or one beyond that,
+    // reads the original K/V row (offset ~0u). Rows at or past the range end
+    // take the original-row path too, whose descriptor reads them as zeros
+    // (their map words are zero-filled padding, not entries).
     const unsigned max_arena_row = 0x80000000u / rb - 1u;
-    unsigned mdec[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) mdec[i] = ~0u;
     // Wave-uniform: some row of the wave's 16-row copy group maps into the
     // arena. Almost every group holds none (an arena covers a few % of a
     // frame's keys), and then neither the per-row decode nor the per-lane
     // choice of source runs: the wave copies like the map-free kernel.
     bool grp_mapped = false;
     // Wave-uniform: every row of the group maps into the arena, to
-    // consecutive arena rows (a run; arena byte offset run_base for the
-    // group's first row). Such a group copies like a plain group, its K and
-    // V descriptors based at that arena row (the frame pipeline's layer
-    // arena holds mapped tiles in key order, so most fully mapped groups are
-    // runs). Not in the non-temporal variant, whose hint must reach original
-    // rows only.
+    // consecutive arena rows (a run). Such a group copies like a plain
+    // group, from the arena, without a per-lane choice of source (the frame
+    // pipeline's layer arena holds mapped tiles in key order, so most fully
+    // mapped groups are runs). Not in the non-temporal variant, whose hint
+    // must reach original rows only.
     constexpr bool kRuns = kMap && !kColdNt;
     bool grp_run = false;
-    unsigned run_base = 0;
+    unsigned run_base = 0;  // arena byte offset of a run's first row
     // arena byte offset of the lane's first copy row within a run
     const unsigned lane_arena = 2u * (unsigned)(lane >> 4) * rb;
-    // Dword 2e+1 of a wave's map slot is the high word of its group's entry e
-    // (row 16*wave + e); an entry can name an arena row only when that word is
-    // 0. Each lane reads one dword of the slot of the next tile to decode
-    // (read_check) as soon as its map copy has landed, at the end of the
-    // iteration before, so the check below waits for nothing.
-    unsigned hw = ~0u;
-    auto read_check = [&](int t) {
+    // hw: lane L < 32 holds word L of the wave's 16 entries (see above); an
+    // entry can name an arena row only when its high word is 0.
+    // A mapped group's copy i reads arena byte offset md[i] (lane's row
+    // ld_row0 + 4i), or the original row where md[i] is ~0u; md is set only
+    // for a mapped group (grp_mapped) and read only by its copies.
+    auto decode_map = [&](int t, unsigned hw, unsigned (&md)[4]) {
         if constexpr (!kMap) return;
-        hw = lds_b32<0>(m_wave + 1024u * (unsigned)(t & 1) + 4u * (unsigned)lane);
-    };
-    auto decode_map = [&](int t) {
-        if constexpr (!kMap) return;
-        const unsigned slot = m_wave + 1024u * (unsigned)(t & 1);
-        const long left = kend - (kbeg + (long)t * kBf16BlockKeys);
+        const int left = nkeys - t * kBf16BlockKeys;
         // rows at or past the range end are zero-filled padding, not entries
         // (a tile past the end has none: valid_rows <= 0)
-        const int valid_rows = left < kBf16BlockKeys ? (int)left : kBf16BlockKeys;
-        lgkm_wait1(hw);
+        const int valid_rows = left < kBf16BlockKeys ? left : kBf16BlockKeys;
         grp_mapped = __builtin_amdgcn_ballot_w64(lane < 32 && (lane & 1) && hw == 0u &&
                                                  16 * wave + (lane >> 1) < valid_rows) != 0;
         grp_run = false;
-        // mdec is read only by the copies of a mixed group (mapped, not a run)
         if (__builtin_expect(!grp_mapped, 1)) return;
         if constexpr (kRuns) {
             // Lanes 0-31 already hold the group's 16 entries (entry e: low
@@ -585,57 +566,62 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_bf16_kernel(AttnArgs a) 
                 grp_run = true;
                 run_base = 2u * l0 * rb;
 #pragma unroll
-                for (int i = 0; i < 4; ++i) mdec[i] = run_base + lane_arena + 8u * (unsigned)i * rb;
+                for (int i = 0; i < 4; ++i) md[i] = run_base + lane_arena + 8u * (unsigned)i * rb;
                 return;
             }
         }
-        const unsigned ad = slot + 8u * (unsigned)(lane >> 4);
-        u32x2 m0 = lds_b64<0>(ad), m1 = lds_b64<32>(ad), m2 = lds_b64<64>(ad), m3 = lds_b64<96>(ad);
-        lgkm_wait_tr(m0, m1, m2, m3);
-        const u32x2 mw[4] = {m0, m1, m2, m3};
+        // copy i of the lane takes row ld_row0 + 4i: entry (lane >> 4) + 4i,
+        // words 2e and 2e+1 fetched from the lanes holding them
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
-            mdec[i] = (ld_row0 + 4 * i < valid_rows && mw[i][1] == 0u && mw[i][0] <= max_arena_row)
-                          ? 2u * mw[i][0] * rb
+        for (int i = 0; i < 4; ++i) {
+            const int e = (lane >> 4) + 4 * i;
+            const unsigned lo = (unsigned)__builtin_amdgcn_ds_bpermute(8 * e, (int)hw);
+            const unsigned hi = (unsigned)__builtin_amdgcn_ds_bpermute(8 * e + 4, (int)hw);
+            md[i] = (ld_row0 + 4 * i < valid_rows && hi == 0u && lo <= max_arena_row)
+                          ? 2u * lo * rb
                           : ~0u;
+        }
     };
-    auto load_map = [&](int t) {
-        if constexpr (!kMap) return;
+    // the map words of tile t (see above); zeros past the range end
+    auto load_map = [&](int t) -> unsigned {
+        if constexpr (!kMap) return ~0u;
         const long t0 = kbeg + (long)t * kBf16BlockKeys;
-        const long left = kend - t0;
         // tiles past the range end (the loop prefetches two ahead) read zeros
-        const int nrec = left <= 0 ? 0 : (int)((left < kBf16BlockKeys ? left : kBf16BlockKeys) * 8);
+        const int nrec = tile_rows_x(t, kBf16BlockKeys * 8, last_rows * 8);
         const __amdgpu_buffer_rsrc_t mrs = __builtin_amdgcn_make_buffer_rsrc(
             const_cast<long*>(map + t0), (short)0, nrec, kBufFlags);
-        KVP_LDS void* md = (KVP_LDS void*)(uintptr_t)(
-            (unsigned)__builtin_amdgcn_readfirstlane((int)m_wave) + 1024u * (unsigned)(t & 1));
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(mrs, md, 4, 128u * wave + 4u * lane, 0, 0, 0);
+        return __builtin_amdgcn_raw_buffer_load_b32(mrs, 128u * wave + 4u * lane, 0, 0);
     };
     // A tile's copies are set up by prep_tile (descriptors and LDS bases)
-    // and issued as 4 K/V pairs by copy_pair(i). Issued back to back, a
-    // wave's 8 copies (1 KiB each) kept it stalled on instruction issue for
-    // about a quarter of every tile on MI355X, while both workgroups of the
-    // CU pushed their 64 KiB through the load path at once; the main loop
-    // instead issues one pair after every second QK k-step of the tile being
-    // computed, so the copies trickle out between MFMAs.
+    // and issued as 4 K/V pairs. Issued back to back, a wave's 8 copies
+    // (1 KiB each) kept it stalled on instruction issue for about a quarter
+    // of every tile on MI355X, while both workgroups of the CU pushed their
+    // 64 KiB through the load path at once; the main loop instead issues one
+    // pair after every second QK k-step of the tile being computed, so the
+    // copies trickle out between MFMAs (copy_plain).
+    // copy_plain(i) reads K at cp_k + i*cp_step + kofs[i] and V at
+    // cp_v + i*cp_step + vofs through krs / vrs into LDS bytes pk + i*pstep
+    // and pv + i*pstep. For a plain group (no KVMap entry) krs / vrs cover
+    // the tile's K / V rows; for a run they both start at the run's first
+    // arena row; for a mixed group (copy_pair fills its rows) the offsets lie
+    // past the tile's records, so these copies read nothing, and they land
+    // in the wave's sink.
     __amdgpu_buffer_rsrc_t krs, vrs;
     unsigned koff = 0, voff = 0;
-    // copy_plain's per-lane offsets: copy i reads K at cp_k + i*cp_step +
-    // kofs[i] and V at cp_v + i*cp_step + vofs through krs / vrs, into LDS
-    // bytes pk + i*pstep and pv + i*pstep
     unsigned cp_k = lane_row, cp_v = lane_row, cp_step = 4u * rb;
     unsigned pk = 0, pv = 0, pstep = 1024u;
     const unsigned sink = (unsigned)(uintptr_t)sink_lds + 2048u * (unsigned)wave;
+    const unsigned lane_arena_v = lane_arena + rb;
     auto prep_tile = [&](int t, unsigned char* kdst, unsigned char* vdst) {
         const long t0 = kbeg + (long)t * kBf16BlockKeys;
-        const long left = kend - t0;
-        // tiles at or past the end (the loop's trailing copies) cover no rows
-        const long rows = left <= 0 ? 0 : (left < kBf16BlockKeys ? left : kBf16BlockKeys);
-        const int nrec = (int)(rows * (long)rb);
-        krs = __builtin_amdgcn_make_buffer_rsrc(const_cast<unsigned char*>(Kb + t0 * (long)rb),
-                                                (short)0, nrec, kBufFlags);
-        vrs = __builtin_amdgcn_make_buffer_rsrc(const_cast<unsigned char*>(Vb + t0 * (long)rb),
-                                                (short)0, nrec, kBufFlags);
+        const unsigned char* kb = Kb + t0 * (long)rb;
+        const unsigned char* vb = Vb + t0 * (long)rb;
+        // tiles past the end (the loop's trailing copies) cover no rows
+        const int nrec = tile_rows_x(t, kBf16BlockKeys * (int)rb, last_rows * (int)rb);
+        krs = __builtin_amdgcn_make_buffer_rsrc(const_cast<unsigned char*>(kb), (short)0, nrec,
+                                                kBufFlags);
+        vrs = __builtin_amdgcn_make_buffer_rsrc(const_cast<unsigned char*>(vb), (short)0, nrec,
+                                                kBufFlags);
         koff = (unsigned)__builtin_amdgcn_readfirstlane((int)(uintptr_t)kdst) + 4096u * wave;
         voff = (unsigned)__builtin_amdgcn_readfirstlane((int)(uintptr_t)vdst) + 4096u * wave;
         cp_k = lane_row;
@@ -645,17 +631,14 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_bf16_kernel(AttnArgs a) 
         pv = voff;
         pstep = 1024u;
         if (kRuns && grp_run) {
-            // [K row | V row] arena rows of the run: 2*rb apart, V rb after K
+            // a run's [K row | V row] arena rows: 2*rb apart, V rb after K
             krs = __builtin_amdgcn_make_buffer_rsrc(
                 const_cast<unsigned char*>(Ab + run_base), (short)0, -1, kBufFlags);
             vrs = krs;
             cp_k = lane_arena;
-            cp_v = lane_arena + rb;
+            cp_v = lane_arena_v;
             cp_step = 8u * rb;
         } else if (kMap && grp_mapped) {
-            // a group mixing arena and original rows (copy_pair fills its
-            // rows): its plain copies aim past the tile's records, so they
-            // read nothing, and land in the wave's sink
             cp_k = kNoRecord;
             cp_v = kNoRecord;
             cp_step = 0;
@@ -664,12 +647,22 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_bf16_kernel(AttnArgs a) 
             pstep = 0;
         }
     };
-    auto copy_pair = [&](int i) {
+    auto copy_plain = [&](int i) {
+        KVP_LDS void* kd = (KVP_LDS void*)(uintptr_t)(pk + pstep * (unsigned)i);
+        KVP_LDS void* vd = (KVP_LDS void*)(uintptr_t)(pv + pstep * (unsigned)i);
+        const unsigned step = (unsigned)i * cp_step;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(krs, kd, 16, cp_k + step + kofs[i], 0, 0,
+                                                 kColdAux);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(vrs, vd, 16, cp_v + step + vofs, 0, 0, kColdAux);
+    };
+    // Copy pair i of any group: each row's source chosen per lane (arena
+    // row where decode_map set an offset, else the original row).
+    auto copy_pair = [&](int i, const unsigned (&md)[4]) {
         KVP_LDS void* kd = (KVP_LDS void*)(uintptr_t)(koff + 1024u * i);
         KVP_LDS void* vd = (KVP_LDS void*)(uintptr_t)(voff + 1024u * i);
         const unsigned row_off = lane_row + 4u * i * rb;
-        if (kMap && mdec[i] != ~0u) {
-            const unsigned ao = mdec[i];
+        if (kMap && md[i] != ~0u) {
+            const unsigned ao = md[i];
             __builtin_amdgcn_raw_ptr_buffer_load_lds(arena_rs, kd, 16, ao + kofs[i], 0, 0, 0);
             __builtin_amdgcn_raw_ptr_buffer_load_lds(arena_rs, vd, 16, ao + rb + vofs, 0, 0, 0);
         } else {
@@ -678,19 +671,6 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_bf16_kernel(AttnArgs a) 
             __builtin_amdgcn_raw_ptr_buffer_load_lds(vrs, vd, 16, row_off + vofs, 0, 0,
                                                      kColdAux);
         }
-    };
-    // The copies interleaved with the QK MFMAs: the map-free kernel's copies
-    // (no per-lane source choice, no branch between the MFMAs), from the
-    // arena for a run. A group mixing arena and original rows, whose rows
-    // copy_pair issued before the tile, sends them past the descriptor's
-    // records (no reads) into its sink.
-    auto copy_plain = [&](int i) {
-        KVP_LDS void* kd = (KVP_LDS void*)(uintptr_t)(pk + pstep * (unsigned)i);
-        KVP_LDS void* vd = (KVP_LDS void*)(uintptr_t)(pv + pstep * (unsigned)i);
-        const unsigned step = (unsigned)i * cp_step;
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(krs, kd, 16, cp_k + step + kofs[i], 0, 0,
-                                                 kColdAux);
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(vrs, vd, 16, cp_v + step + vofs, 0, 0, kColdAux);
     };
 
     f32x16 o[4];
@@ -788,12 +768,12 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_bf16_kernel(AttnArgs a) 
             s[v] = s0[v];
             s[16 + v] = s1[v];
         }
-        const long t0 = kbeg + (long)t * kBf16BlockKeys;
-        if (t0 + kBf16BlockKeys > kend) {
+        const int left = nkeys - t * kBf16BlockKeys;
+        if (left < kBf16BlockKeys) {
             // s[v] holds key kc(v) + 4*hh of the tile, kc(v) a compile-time
             // constant: comparing kc(v) with lim - 4*hh keeps the per-lane
             // key indices out of registers.
-            const int lim = (int)(kend - t0) - 4 * hh;
+            const int lim = left - 4 * hh;
 #pragma unroll
             for (int v = 0; v < 32; ++v) {
                 const int kc = 32 * (v >> 4) + 8 * ((v & 15) >> 2) + (v & 3);
@@ -879,20 +859,19 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_bf16_kernel(AttnArgs a) 
         __builtin_amdgcn_s_setprio(0);
     };
 
+    unsigned hw_next = ~0u;  // map words of the tile after the next one
     if (ntiles > 0) {
-        load_map(0);
-        wait_vm<0>();
-        read_check(0);
-        decode_map(0);
-        load_map(1);
+        const unsigned hw0 = load_map(0);
+        hw_next = load_map(1);
+        unsigned md[4] = {~0u, ~0u, ~0u, ~0u};
+        decode_map(0, hw0, md);
         prep_tile(0, k_lds0, v_lds0);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) copy_pair(i);
+        for (int i = 0; i < 4; ++i) copy_pair(i, md);
     }
     // Compiler-visible wait for every load so far (Q, map, tile 0): the loop
     // then never waits for vector memory on the Q registers' account.
     __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
-    if (ntiles > 0) read_check(1);
     for (int t = 0; t < ntiles; ++t) {
         // tile t lives in stage t & 1; tile t+1 streams into the other stage,
         // which every wave finished reading before the barrier that closed
@@ -901,17 +880,19 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_bf16_kernel(AttnArgs a) 
         unsigned char* vcur = (t & 1) ? v_lds1 : v_lds0;
         unsigned char* knext = (t & 1) ? k_lds0 : k_lds1;
         unsigned char* vnext = (t & 1) ? v_lds0 : v_lds1;
-        // each wave's copies of tile t (and map copies) have landed, then
+        // each wave's copies of tile t (and its map load) have landed, then
         // the barrier publishes the whole tile
         wait_vm<0>();
         wg_barrier();
-        // The copies for tile t+1 and the map copy for tile t+2 are issued
+        // The copies for tile t+1 and the map load for tile t+2 are issued
         // unconditionally, so the QK k-steps they sit between stay one basic
         // block: past the last tile the descriptors cover no rows (every row
         // and map word reads as zero) and no KVMap entry is decoded (rows past
         // the range end are not entries).
-        decode_map(t + 1);
-        load_map(t + 2);
+        const unsigned hw1 = hw_next;
+        hw_next = load_map(t + 2);
+        unsigned md[4];
+        decode_map(t + 1, hw1, md);
         prep_tile(t + 1, knext, vnext);
         // wave-uniform: the group mixes arena and original rows, each row's
         // source chosen per lane (copy_pair)
@@ -919,25 +900,17 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_bf16_kernel(AttnArgs a) 
         if (active) {
             if (__builtin_expect(mixed, 0)) {
 #pragma unroll
-                for (int i = 0; i < 4; ++i) copy_pair(i);
+                for (int i = 0; i < 4; ++i) copy_pair(i, md);
             }
             compute_tile(t, kcur, vcur, [&](int ks) {
                 if ((ks & 1) == 0) copy_plain(ks >> 1);
             });
         } else if (mixed) {
 #pragma unroll
-            for (int i = 0; i < 4; ++i) copy_pair(i);
+            for (int i = 0; i < 4; ++i) copy_pair(i, md);
         } else {
 #pragma unroll
             for (int i = 0; i < 4; ++i) copy_plain(i);
-        }
-        if constexpr (kMap) {
-            // the map copy of tile t+2 was issued before this iteration's
-            // tile copies (8, or 16 for a mixed group whose last 8 go to
-            // the sink), so once at most 8 loads are outstanding it has
-            // landed
-            wait_vm<8>();
-            read_check(t + 2);
         }
         wg_barrier();
     }
