@@ -571,15 +571,20 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_bf16_kernel(AttnArgs a) 
             }
         }
         // copy i of the lane takes row ld_row0 + 4i: entry (lane >> 4) + 4i,
-        // words 2e and 2e+1 fetched from the lanes holding them
+        // words 2e and 2e+1 fetched from the lanes holding them (all eight
+        // fetches in flight together, then one branch-free decode)
+        unsigned lo[4], hi[4];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const int e = (lane >> 4) + 4 * i;
-            const unsigned lo = (unsigned)__builtin_amdgcn_ds_bpermute(8 * e, (int)hw);
-            const unsigned hi = (unsigned)__builtin_amdgcn_ds_bpermute(8 * e + 4, (int)hw);
-            md[i] = (ld_row0 + 4 * i < valid_rows && hi == 0u && lo <= max_arena_row)
-                          ? 2u * lo * rb
-                          : ~0u;
+            lo[i] = (unsigned)__builtin_amdgcn_ds_bpermute(8 * e, (int)hw);
+            hi[i] = (unsigned)__builtin_amdgcn_ds_bpermute(8 * e + 4, (int)hw);
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const bool ok = (ld_row0 + 4 * i < valid_rows) & (hi[i] == 0u) &
+                            (lo[i] <= max_arena_row);
+            md[i] = ok ? 2u * lo[i] * rb : ~0u;
         }
     };
     // the map words of tile t (see above); zeros past the range end
