@@ -879,8 +879,8 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_bf16_kernel(AttnArgs a) 
     __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
     for (int t = 0; t < ntiles; ++t) {
         // tile t lives in stage t & 1; tile t+1 streams into the other stage,
-        // which every wave finished reading before the barrier that closed
-        // the previous iteration
+        // which held tile t-1: every wave finished reading it before it
+        // reached the barrier below, so one barrier per tile suffices
         unsigned char* kcur = (t & 1) ? k_lds1 : k_lds0;
         unsigned char* vcur = (t & 1) ? v_lds1 : v_lds0;
         unsigned char* knext = (t & 1) ? k_lds0 : k_lds1;
@@ -917,14 +917,16 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_bf16_kernel(AttnArgs a) 
 #pragma unroll
             for (int i = 0; i < 4; ++i) copy_plain(i);
         }
-        wg_barrier();
     }
-    // the trailing copies land before the workgroup's LDS is released
+    // the trailing copies land before the workgroup's LDS is released, and
+    // every wave has read its last tile before the epilogue stages output
+    // rows there
     wait_vm<0>();
+    wg_barrier();
     if (!active) return;
 
-    // Stage in the last tile's stage: every wave has passed the barrier that
-    // closed its last read, and the trailing copies target the other stage.
+    // Stage in the last tile's stage: every wave has passed the barrier
+    // after its last read, and the trailing copies target the other stage.
     unsigned char* last_k = (ntiles > 0 && ((ntiles - 1) & 1)) ? k_lds1 : k_lds0;
     unsigned char* last_v = (ntiles > 0 && ((ntiles - 1) & 1)) ? v_lds1 : v_lds0;
     unsigned char* stage = (wave < 2 ? last_k : last_v) + 8192 * (wave & 1);
