@@ -157,28 +157,47 @@ __global__ __launch_bounds__(kLayerThreads) void layer_stage_kernel(
     }
 }
 
+// Descriptor ring in mapped, coherent host memory: the host writes a
+// launch's run descriptors at `head`, the staging kernel reads them over
+// the bus. A region is written again only after the ring wraps, and the
+// wrap first waits for every launch that read the ring (drain). No event is
+// recorded per launch: on MI355X an event record between the staging
+// kernel and the attention launch after it, with its system-scope fence,
+// left the GPU idle for about 5.6 us before the next kernel.
 struct Stager {
     unsigned char* host = nullptr;  // mapped pinned memory
     unsigned char* dev = nullptr;   // device view of `host`
     size_t cap = 0;
     size_t head = 0;
-    std::vector<hipEvent_t> inflight;
-    std::vector<hipEvent_t> spare;
+    hipStream_t last = nullptr;  // stream of the launches since the last drain
+    bool pending = false;        // launches since the last drain may still run
 
     ~Stager() {
-        drain();
-        for (hipEvent_t e : spare) (void)hipEventDestroy(e);
+        // the caller's stream may be gone by now: wait for the whole device
+        if (pending) (void)hipDeviceSynchronize();
         if (host) (void)hipHostFree(host);
     }
-    bool drain() {
-        bool ok = true;
-        for (hipEvent_t e : inflight) {
-            if (hipEventSynchronize(e) != hipSuccess) ok = false;
-            spare.push_back(e);
+    // Call before a launch on `s` that reads the ring. A launch on another
+    // stream than the pending ones first waits for the device: the earlier
+    // stream is not used again, as it may have been destroyed.
+    bool before_launch(hipStream_t s) {
+        if (pending && s != last) {
+            if (hipDeviceSynchronize() != hipSuccess) return false;
+            pending = false;
         }
-        inflight.clear();
+        last = s;
+        return true;
+    }
+    void after_launch() { pending = true; }
+    // Waits for every launch that read the ring (all on `last`), then
+    // restarts at its beginning.
+    bool drain() {
+        if (pending) {
+            if (hipStreamSynchronize(last) != hipSuccess) return false;
+            pending = false;
+        }
         head = 0;
-        return ok;
+        return true;
     }
     bool reserve(size_t need) {
         if (need > cap) {
@@ -188,7 +207,8 @@ struct Stager {
             dev = nullptr;
             cap = 0;
             size_t want = need < ((size_t)4 << 20) ? ((size_t)4 << 20) : need * 2;
-            if (hipHostMalloc(reinterpret_cast<void**>(&host), want, hipHostMallocMapped) != hipSuccess) {
+            if (hipHostMalloc(reinterpret_cast<void**>(&host), want,
+                              hipHostMallocMapped | hipHostMallocCoherent) != hipSuccess) {
                 host = nullptr;
                 return false;
             }
@@ -204,16 +224,6 @@ struct Stager {
             if (!drain()) return false;
         }
         return true;
-    }
-    hipEvent_t take_event() {
-        if (!spare.empty()) {
-            hipEvent_t e = spare.back();
-            spare.pop_back();
-            return e;
-        }
-        hipEvent_t e = nullptr;
-        if (hipEventCreateWithFlags(&e, hipEventDisableTiming) != hipSuccess) return nullptr;
-        return e;
     }
 };
 
@@ -352,7 +362,7 @@ int kvp_stage_run(void* stager, void* arena, long row_stride_bytes, const KvpRow
     long* d_rows = nullptr;
     long* d_slots = nullptr;
     if (need > 0) {
-        if (!st->reserve(need)) {
+        if (!st->before_launch(hs) || !st->reserve(need)) {
             set_error("stage: descriptor ring allocation failed");
             return 1;
         }
@@ -386,14 +396,7 @@ int kvp_stage_run(void* stager, void* arena, long row_stride_bytes, const KvpRow
         return 1;
     }
     if (need > 0) {
-        hipEvent_t ev = st->take_event();
-        if (!ev || hipEventRecord(ev, hs) != hipSuccess) {
-            // Without a fence the region cannot be reused safely: drain now.
-            if (ev) st->spare.push_back(ev);
-            (void)hipStreamSynchronize(hs);
-        } else {
-            st->inflight.push_back(ev);
-        }
+        st->after_launch();
         st->head += need;
     }
     return 0;
@@ -492,7 +495,8 @@ int layer_stage_launch(void* stager, void* arena, const void* k, const void* v, 
     }
     const size_t copy_bytes = align256((size_t)n_copies * sizeof(LayerCopyRun));
     const size_t need = copy_bytes + align256((size_t)n_map_runs * sizeof(LayerMapRun));
-    if (!st->reserve(need)) {
+    hipStream_t hs = static_cast<hipStream_t>(stream);
+    if (!st->before_launch(hs) || !st->reserve(need)) {
         set_error("layer stage: descriptor ring allocation failed");
         return 1;
     }
@@ -500,7 +504,6 @@ int layer_stage_launch(void* stager, void* arena, const void* k, const void* v, 
     unsigned char* d = st->dev + st->head;
     if (n_copies > 0) memcpy(h, copies, (size_t)n_copies * sizeof(LayerCopyRun));
     if (n_map_runs > 0) memcpy(h + copy_bytes, map_runs, (size_t)n_map_runs * sizeof(LayerMapRun));
-    hipStream_t hs = static_cast<hipStream_t>(stream);
     hipLaunchKernelGGL(layer_stage_kernel, dim3((unsigned)(n_copies + n_map_runs)),
                        dim3(kLayerThreads), 0, hs, reinterpret_cast<const LayerCopyRun*>(d),
                        n_copies, reinterpret_cast<const LayerMapRun*>(d + copy_bytes),
@@ -511,13 +514,7 @@ int layer_stage_launch(void* stager, void* arena, const void* k, const void* v, 
         set_error("layer stage launch: %s", hipGetErrorString(e));
         return 1;
     }
-    hipEvent_t ev = st->take_event();
-    if (!ev || hipEventRecord(ev, hs) != hipSuccess) {
-        if (ev) st->spare.push_back(ev);
-        (void)hipStreamSynchronize(hs);
-    } else {
-        st->inflight.push_back(ev);
-    }
+    st->after_launch();
     st->head += need;
     return 0;
 }

@@ -23,10 +23,10 @@ KVTileManager::KVTileManager(size_t budget_bytes, size_t max_window_bytes)
 KVTileManager::~KVTileManager() {
     clear();
     // Pending copies still land (an attached arena outlives the manager);
-    // then the descriptor ring drains its fences before memory is freed.
+    // then the descriptor ring waits for its launches before it is freed.
     flush();
     if (stager_) {
-        kvp_stager_destroy(stager_);  // drains its fences
+        kvp_stager_destroy(stager_);  // waits for the launches that read it
         stager_ = nullptr;
     }
     if (arena_ && arena_owned_) {

@@ -209,8 +209,9 @@ int kvp_memcpy_d2d(void* dst, const void* src, size_t bytes, void* stream);
 int kvp_stream_sync(void* stream);
 int kvp_device_sync(void);
 
-/* Staging ring: pinned host + device descriptor buffers reused across
- * flushes with event fences. */
+/* Staging ring: mapped coherent host memory holding the launches' run
+ * descriptors, reused across flushes; when it wraps it first waits for the
+ * launches that read it (destroying a stager waits for the device). */
 void* kvp_stager_create(void);
 void kvp_stager_destroy(void* stager);
 /* One flush: optional map rebuild (map_dev[0..map_fill) = -1 then
