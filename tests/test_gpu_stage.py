@@ -111,3 +111,53 @@ def test_stage_run_unaligned_rows_use_byte_copies():
         assert torch.equal(arena, _expect(torch.zeros(16, 2 * D, device=DEV), D, K, V, src, dst))
     finally:
         lib.kvp_stager_destroy(stager)
+
+
+def test_stage_ring_wraps_and_changes_stream_without_host_waits():
+    """120 descriptor-ring flushes of ~96 KB each (the 4 MiB ring wraps twice),
+    issued back to back with no host synchronisation, the first 60 on
+    one stream and the rest on another: the ring reuses a region only after
+    the launches that read it have finished, and a change of stream waits
+    for the earlier one, so the arena and the KVMap end as a sequential
+    replay of the flushes leaves them."""
+    lib = _lib.load()
+    D, N, A, n = 256, 4096, 4096, 2000
+    dtype = torch.bfloat16
+    g = torch.Generator(device="cpu").manual_seed(21)
+    K = torch.randn(N, D, generator=g).to(dtype)
+    V = torch.randn(N, D, generator=g).to(dtype)
+    Kd, Vd = K.to(DEV), V.to(DEV)
+    arena = torch.zeros(A, 2 * D, dtype=dtype, device=DEV)
+    kvmap = torch.full((N,), -1, dtype=torch.long, device=DEV)
+    exp_arena = torch.zeros(A, 2 * D, dtype=dtype)
+    exp_map = torch.full((N,), -1, dtype=torch.long)
+    kb = D * K.element_size()
+    stride = 2 * kb
+    rng = np.random.default_rng(8)
+    streams = [torch.cuda.Stream(), torch.cuda.Stream()]
+    keep = []  # host descriptor arrays stay alive until the end
+    stager = lib.kvp_stager_create()
+    try:
+        for i in range(120):
+            src = rng.choice(N, size=n, replace=True)
+            dst = rng.choice(A, size=n, replace=False)
+            arr = (KvpRowCopy * n)()
+            for j in range(n):
+                arr[j] = KvpRowCopy(Kd.data_ptr() + int(src[j]) * kb,
+                                    Vd.data_ptr() + int(src[j]) * kb, int(dst[j]), kb, kb)
+            mr = rng.choice(N, size=n, replace=False).astype(np.int64)
+            ms = rng.integers(-1, A, size=n).astype(np.int64)
+            keep.append((arr, mr, ms))
+            st = streams[0 if i < 60 else 1]
+            rc = lib.kvp_stage_run(stager, arena.data_ptr(), stride, ctypes.cast(arr, ctypes.c_void_p),
+                                   n, kvmap.data_ptr(), 0, mr.ctypes.data, ms.ctypes.data, n,
+                                   ctypes.c_void_p(st.cuda_stream))
+            assert rc == 0, lib.kvp_last_error()
+            exp_arena[torch.from_numpy(dst)] = torch.cat([K[torch.from_numpy(src)],
+                                                          V[torch.from_numpy(src)]], dim=1)
+            exp_map[torch.from_numpy(mr)] = torch.from_numpy(ms)
+        torch.cuda.synchronize()
+        assert torch.equal(arena.cpu(), exp_arena)
+        assert torch.equal(kvmap.cpu(), exp_map)
+    finally:
+        lib.kvp_stager_destroy(stager)
