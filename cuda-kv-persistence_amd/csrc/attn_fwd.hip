@@ -687,6 +687,21 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_bf16_kernel(AttnArgs a) 
     float l_run = 0.f;
     const float cl2 = a.scale_log2;
 
+    // Row sums of a tile's P on the matrix core: P^T fragment g (the B
+    // operand of the PV MFMA: lane l holds keys 16g + 8*(l/32) + 0..7 of
+    // query l % 32) read as the B operand of a 16x16x32 MFMA puts those
+    // values in row group k/8 = l/16 of column n = l % 16. With A[m][k] = 1
+    // where bit 0 of k/8 equals bit 0 of m (else 0), D[m][n] sums the 16 keys
+    // of query n (m even: lanes n and n+32) or of query n + 16 (m odd: lanes
+    // n+16 and n+48); lane l reads D[4*(l/16) + v][l % 16] in acc[v], so its
+    // own query's sum is acc[(l/16) & 1]. Four such MFMAs (one per k-step)
+    // replace 32 VALU adds and a cross-half exchange per tile, and the sum
+    // is of the bf16 weights the PV product uses.
+    const bool rs_hi = (lane >> 4) & 1;
+    bf16x8 rsel;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) rsel[i] = (((lane >> 4) ^ lane) & 1) ? (__bf16)0.f : (__bf16)1.f;
+
     // Per-lane parts of the LDS read addresses.
     const unsigned kswz = (unsigned)(lq & 15);
     const int grp = lane >> 4;
@@ -790,14 +805,13 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_bf16_kernel(AttnArgs a) 
         // overflows the bound (first tile, where the running max is -inf, or
         // scores that grew far beyond it) take the slow path: raise the max
         // to the tile max, rescale O and l, and exponentiate again.
-        // The row sum adds the fp32 exponentials with plain VALU adds: the
-        // packed bf16 dot instruction would sum the rounded P exactly, but on
-        // gfx950 it does not issue while the other wave of the SIMD streams
-        // MFMAs (measured), which stalls this softmax behind the other
-        // wave's matrix work.
+        // The tile's row sum comes from the matrix core (rsel above), so
+        // the VALU work per score is one FMA, one exponential and half a
+        // bf16 pack. (A 0 x inf product in that sum, from an infinite
+        // exponential, yields NaN, which fails the bound check as the inf
+        // itself would.)
         bf16x8 pb[4];
         auto exp_tile = [&](float mref) {
-            float rs = 0.f;
 #pragma unroll
             for (int g = 0; g < 4; ++g) {
 #pragma unroll
@@ -806,12 +820,13 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_bf16_kernel(AttnArgs a) 
                     const float e1 = fast_exp2(fmaf(s[8 * g + i + 1], cl2, -mref));
                     pb[g][i] = (__bf16)e0;
                     pb[g][i + 1] = (__bf16)e1;
-                    rs += e0 + e1;
                 }
             }
-            float rlo, rhi;
-            swap_halves(rs, rlo, rhi);
-            return rlo + rhi;
+            f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int g = 0; g < 4; ++g)
+                acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(rsel, pb[g], acc, 0, 0, 0);
+            return rs_hi ? acc[1] : acc[0];
         };
         float tot = exp_tile(m_run);
         if (__builtin_amdgcn_ballot_w64(!(tot <= kRowSumLimit))) {
