@@ -95,6 +95,7 @@ struct AttnArgs {
     int splits;
     int nqb;
     int layer_order;   // 1: XCD-column work order, frames longest first
+    int xcd_slots;     // layer order: workgroups one XCD runs at once (0: unknown)
     float scale_log2;  // log2(e) / sqrt(head_dim)
 };
 
@@ -110,6 +111,7 @@ __device__ __forceinline__ int xcd_remap(int bid, int n) {
 struct WgCoord {
     int qb, split, head, frame;
     bool valid;
+    bool rev;  // visit the key tiles last to first
 };
 
 // Number of (head, q-block) columns XCD x owns in the layer work order.
@@ -121,6 +123,7 @@ __device__ __forceinline__ WgCoord decode_wg(const AttnArgs& a) {
     WgCoord c;
     c.valid = true;
     c.split = 0;
+    c.rev = false;
     if (a.layer_order) {
         // Layer work order. The hardware hands workgroup b to XCD b % 8, so
         // XCD x runs workgroups x, x+8, x+16, ... in that order. XCD x owns
@@ -139,6 +142,14 @@ __device__ __forceinline__ WgCoord decode_wg(const AttnArgs& a) {
         }
         const int col = x * cols / kNumXcd + j % n;
         c.frame = a.frames - 1 - j / n;
+        // The first xcd_slots workgroups of an XCD start together and walk
+        // their keys upward from key 0 in step, so each K/V tile is fetched
+        // once for all of them. A later workgroup starts when an earlier one
+        // ends, with the long ranges still running near their top: it walks
+        // its keys downward from its range end, through the tiles the
+        // running workgroups fetched last (still in the L2), instead of
+        // restarting at key 0, whose tiles the L2 has long evicted.
+        c.rev = a.xcd_slots > 0 && j >= a.xcd_slots;
         c.head = col / a.nqb;
         c.qb = col % a.nqb;
         return c;
@@ -460,9 +471,21 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_bf16_kernel(AttnArgs a) 
     // nkeys - 64*t becomes a vector min/max here, and a descriptor built
     // from a vector value is taken apart lane by lane).
     const int last_rows = nkeys - (ntiles - 1) * kBf16BlockKeys;
+    // Tiles outside [0, ntiles) -- the loop's prefetches past either end of
+    // the walk -- have no rows.
     auto tile_rows_x = [&](int t, int full, int last) {
-        return t < ntiles - 1 ? full : (t == ntiles - 1 ? last : 0);
+        return (unsigned)t < (unsigned)(ntiles - 1) ? full : (t == ntiles - 1 ? last : 0);
     };
+    // Key tile visited at loop step i: upward, or downward for a reversed
+    // workgroup (decode_wg); steps past the walk map outside [0, ntiles).
+    // The first key of step i's tile is computed in 64 bits from i itself
+    // (key_first + i * key_step), so that the tile addresses stay induction
+    // variables of the loop.
+    const int t_first = c.rev ? ntiles - 1 : 0;
+    const int t_dir = c.rev ? -1 : 1;
+    auto tix = [&](int i) { return t_first + t_dir * i; };
+    const long key_first = kbeg + (long)t_first * kBf16BlockKeys;
+    const long key_step = (long)t_dir * kBf16BlockKeys;
 
     const __bf16* Q = reinterpret_cast<const __bf16*>(a.q) + (long)c.frame * a.q_fstride;
     const unsigned char* Kb = reinterpret_cast<const unsigned char*>(a.k) + 2L * c.frame * a.kv_fstride;
@@ -545,10 +568,9 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_bf16_kernel(AttnArgs a) 
     // for a mapped group (grp_mapped) and read only by its copies.
     auto decode_map = [&](int t, unsigned hw, unsigned (&md)[4]) {
         if constexpr (!kMap) return;
-        const int left = nkeys - t * kBf16BlockKeys;
         // rows at or past the range end are zero-filled padding, not entries
-        // (a tile past the end has none: valid_rows <= 0)
-        const int valid_rows = left < kBf16BlockKeys ? left : kBf16BlockKeys;
+        // (a tile outside the range has none)
+        const int valid_rows = tile_rows_x(t, kBf16BlockKeys, last_rows);
         grp_mapped = __builtin_amdgcn_ballot_w64(lane < 32 && (lane & 1) && hw == 0u &&
                                                  16 * wave + (lane >> 1) < valid_rows) != 0;
         grp_run = false;
@@ -587,11 +609,14 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_bf16_kernel(AttnArgs a) 
             md[i] = ok ? 2u * lo[i] * rb : ~0u;
         }
     };
-    // the map words of tile t (see above); zeros past the range end
-    auto load_map = [&](int t) -> unsigned {
+    // the map words of step i's tile (see above); zeros outside the range
+    auto load_map = [&](int i) -> unsigned {
         if constexpr (!kMap) return ~0u;
-        const long t0 = kbeg + (long)t * kBf16BlockKeys;
-        // tiles past the range end (the loop prefetches two ahead) read zeros
+        const int t = tix(i);
+        // outside the range (at most two tiles beyond either end) the base
+        // is past the slice, but the descriptor has no records to read
+        const long t0 = key_first + (long)i * key_step;
+        // tiles outside the range (the loop prefetches two ahead) read zeros
         const int nrec = tile_rows_x(t, kBf16BlockKeys * 8, last_rows * 8);
         const __amdgpu_buffer_rsrc_t mrs = __builtin_amdgcn_make_buffer_rsrc(
             const_cast<long*>(map + t0), (short)0, nrec, kBufFlags);
@@ -617,11 +642,12 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_bf16_kernel(AttnArgs a) 
     unsigned pk = 0, pv = 0, pstep = 1024u;
     const unsigned sink = (unsigned)(uintptr_t)sink_lds + 2048u * (unsigned)wave;
     const unsigned lane_arena_v = lane_arena + rb;
-    auto prep_tile = [&](int t, unsigned char* kdst, unsigned char* vdst) {
-        const long t0 = kbeg + (long)t * kBf16BlockKeys;
+    auto prep_tile = [&](int i, unsigned char* kdst, unsigned char* vdst) {
+        const int t = tix(i);
+        const long t0 = key_first + (long)i * key_step;
         const unsigned char* kb = Kb + t0 * (long)rb;
         const unsigned char* vb = Vb + t0 * (long)rb;
-        // tiles past the end (the loop's trailing copies) cover no rows
+        // tiles outside the range (the loop's trailing copies) cover no rows
         const int nrec = tile_rows_x(t, kBf16BlockKeys * (int)rb, last_rows * (int)rb);
         krs = __builtin_amdgcn_make_buffer_rsrc(const_cast<unsigned char*>(kb), (short)0, nrec,
                                                 kBufFlags);
@@ -884,7 +910,7 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_bf16_kernel(AttnArgs a) 
         const unsigned hw0 = load_map(0);
         hw_next = load_map(1);
         unsigned md[4] = {~0u, ~0u, ~0u, ~0u};
-        decode_map(0, hw0, md);
+        decode_map(tix(0), hw0, md);
         prep_tile(0, k_lds0, v_lds0);
 #pragma unroll
         for (int i = 0; i < 4; ++i) copy_pair(i, md);
@@ -893,26 +919,27 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_bf16_kernel(AttnArgs a) 
     // then never waits for vector memory on the Q registers' account.
     __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
     for (int t = 0; t < ntiles; ++t) {
-        // tile t lives in stage t & 1; tile t+1 streams into the other stage,
-        // which held tile t-1: every wave finished reading it before it
+        // t counts loop steps; step t computes tile tix(t). Step t's tile
+        // lives in stage t & 1; step t+1's tile streams into the other stage,
+        // which held step t-1's: every wave finished reading it before it
         // reached the barrier below, so one barrier per tile suffices
         unsigned char* kcur = (t & 1) ? k_lds1 : k_lds0;
         unsigned char* vcur = (t & 1) ? v_lds1 : v_lds0;
         unsigned char* knext = (t & 1) ? k_lds0 : k_lds1;
         unsigned char* vnext = (t & 1) ? v_lds0 : v_lds1;
-        // each wave's copies of tile t (and its map load) have landed, then
-        // the barrier publishes the whole tile
+        // each wave's copies of step t's tile (and its map load) have
+        // landed, then the barrier publishes the whole tile
         wait_vm<0>();
         wg_barrier();
-        // The copies for tile t+1 and the map load for tile t+2 are issued
+        // The copies for step t+1 and the map load for step t+2 are issued
         // unconditionally, so the QK k-steps they sit between stay one basic
-        // block: past the last tile the descriptors cover no rows (every row
-        // and map word reads as zero) and no KVMap entry is decoded (rows past
-        // the range end are not entries).
+        // block: past the end of the walk the descriptors cover no rows
+        // (every row and map word reads as zero) and no KVMap entry is
+        // decoded (rows outside the range are not entries).
         const unsigned hw1 = hw_next;
         hw_next = load_map(t + 2);
         unsigned md[4];
-        decode_map(t + 1, hw1, md);
+        decode_map(tix(t + 1), hw1, md);
         prep_tile(t + 1, knext, vnext);
         // wave-uniform: the group mixes arena and original rows, each row's
         // source chosen per lane (copy_pair)
@@ -922,7 +949,7 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_bf16_kernel(AttnArgs a) 
 #pragma unroll
                 for (int i = 0; i < 4; ++i) copy_pair(i, md);
             }
-            compute_tile(t, kcur, vcur, [&](int ks) {
+            compute_tile(tix(t), kcur, vcur, [&](int ks) {
                 if ((ks & 1) == 0) copy_plain(ks >> 1);
             });
         } else if (mixed) {
@@ -1587,6 +1614,10 @@ int prepare_launch(const AttnLaunch& L, const DeviceInfo& di, AttnArgs& a, Launc
     a.splits = p.splits;
     a.nqb = p.nqb;
     a.layer_order = layer ? 1 : 0;
+    // Only the bf16 kernel reverses later workgroups (the fp32 kernel walks
+    // every range upward); the count assumes the occupancy the kernel was
+    // measured at, and only steers the order, never correctness.
+    a.xcd_slots = layer && L.dtype == 1 ? std::max(1, di.cus / kNumXcd) * di.wg_per_cu_bf16 : 0;
     a.scale_log2 = kLog2e / sqrtf((float)kHeadDim);
     return 0;
 }

@@ -4,6 +4,9 @@ edge cases, through the C-ABI.
 * kvp_attn_forward_frames (every frame of a layer in one grid, frame f
   reading its own arena region and KVMap slice) against the CPU oracle,
   and bitwise equal to the same launch without a map.
+* At C3's layer shape, where later workgroups walk their keys last to
+  first, sampled rows of every frame match the oracle and a KVMap is
+  bitwise invisible.
 * Key rows past the end of a partial last tile never read the arena: an
   arena whose row 0 holds NaN leaves the output finite and bitwise equal to
   the map-free launch (T = 1560 is not a multiple of the 64-key tile).
@@ -191,6 +194,44 @@ def test_layer_launch_equals_single_frame_launches_within_tolerance(dtype):
     torch.cuda.synchronize()
     tol = 2e-5 if dtype == torch.float32 else 1.6e-2
     assert float((per.float() - layer).abs().max()) <= tol
+
+
+@pytest.mark.parametrize("mode,window", [("cross", 0), ("cross", 3)])
+def test_reversed_key_walks_match_oracle_and_map_is_invisible(mode, window):
+    """C3's layer shape (8 x 1560, 12 heads: 1,248 workgroups, more than an
+    MI355X XCD runs at once), so the workgroups that start after an XCD's
+    first round walk their key tiles last to first: sampled query rows of
+    every frame (first, middle and tail q-blocks) against the oracle; a KVMap
+    with random arena rows is bitwise invisible; an arena whose row 0 holds
+    NaN, with a sparse map that never names it, leaves the output finite and
+    bitwise equal to the map-free launch."""
+    frames, T, heads = 8, 1560, 12
+    D = heads * 128
+    q, k, v = _inputs(frames, T, heads, seed=1248 + window, dtype=torch.bfloat16)
+    qd, kd, vd = (x.to(DEV).to(torch.bfloat16).contiguous() for x in (q, k, v))
+    base = _layer(torch.bfloat16, qd, kd, vd, frames, T, heads, mode, window)
+    got_all = base.float().cpu()
+    for f in range(frames):
+        b, e = at.key_range(mode, f, T, window)
+        rows = np.r_[0:8, 700:708, T - 24:T] + f * T
+        want = at.attention_keys(q[rows], k[b:e], v[b:e], heads)
+        _check(got_all[rows], want, torch.bfloat16)
+    rng = np.random.default_rng(99 + window)
+    region_rows = 96
+    arena, kvmap, stride = _layer_arenas(k.to(torch.bfloat16), v.to(torch.bfloat16), frames, T,
+                                         mode, window, rng, region_rows)
+    region_bytes = region_rows * 2 * D * 2
+    got = _layer(torch.bfloat16, qd, kd, vd, frames, T, heads, mode, window, arena.to(DEV),
+                 kvmap.to(DEV), region_bytes, stride)
+    assert torch.equal(got, base)
+    # slot 0 of every region unused by the map and poisoned
+    kvmap = torch.where(kvmap == 0, torch.full_like(kvmap, -1), kvmap)
+    for f in range(frames):
+        arena[f * region_rows] = float("nan")
+    got = _layer(torch.bfloat16, qd, kd, vd, frames, T, heads, mode, window, arena.to(DEV),
+                 kvmap.to(DEV), region_bytes, stride)
+    assert bool(torch.isfinite(got.float()).all())
+    assert torch.equal(got, base)
 
 
 @pytest.mark.parametrize("api_kind", ["single_frame", "layer"])
