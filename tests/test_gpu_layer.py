@@ -110,14 +110,17 @@ def test_kvmap_reads_the_arena_row_the_map_names(dtype, api_kind):
     """Arena rows hold other data than the key rows they stand in for: the
     output must be attention over K/V with every mapped row replaced by its
     arena row (reference semantics, src/gated_attention_kernel.cu:73-85 and
-    :118-130), including rows in the last, partial key tile."""
+    :118-130), including rows in the last, partial key tile and two aligned
+    16-row groups mapped to consecutive arena rows (the kernel's run path)."""
     frames, T, heads = 3, 1560, 2
     D = heads * 128
     q, k, v = _inputs(frames, T, heads, seed=29, dtype=dtype)
     rng = np.random.default_rng(29)
     region_rows = 200
+    run_rows, run_slot0 = range(128, 160), region_rows  # slots past the permuted ones
     full = frames * T
-    arena = torch.from_numpy(rng.standard_normal((frames * region_rows, 2 * D),
+    region_total = region_rows + len(run_rows)
+    arena = torch.from_numpy(rng.standard_normal((frames * region_total, 2 * D),
                                                  dtype=np.float32))
     if dtype == torch.bfloat16:
         arena = at.round_bf16(arena)
@@ -128,26 +131,28 @@ def test_kvmap_reads_the_arena_row_the_map_names(dtype, api_kind):
         # whole 16-row groups, single rows, and rows of the last partial tile
         rows = set(rng.choice(e, size=120, replace=False).tolist())
         rows |= set(range(e - 20, e)) | set(range(64, 80))
-        rows = sorted(rows)[:region_rows]
-        slots = rng.permutation(region_rows)[:len(rows)]
+        rows = sorted(rows - set(run_rows))[:region_rows]
+        slots = list(rng.permutation(region_rows)[:len(rows)])
+        rows += list(run_rows)
+        slots += [run_slot0 + i for i in range(len(run_rows))]
         kf, vf = k[:e].clone(), v[:e].clone()
         for r, sl in zip(rows, slots):
             kvmap[f * full + r] = int(sl)
-            kf[r] = arena[f * region_rows + sl, :D]
-            vf[r] = arena[f * region_rows + sl, D:]
+            kf[r] = arena[f * region_total + sl, :D]
+            vf[r] = arena[f * region_total + sl, D:]
         want[f * T:e] = at.attention_keys(q[f * T:e], kf, vf, heads)
     qd, kd, vd = (x.to(DEV).to(dtype).contiguous() for x in (q, k, v))
     ad, md = arena.to(DEV).to(dtype), kvmap.to(DEV)
     if api_kind == "layer":
         got = _layer(dtype, qd, kd, vd, frames, T, heads, "cross", 0, ad, md,
-                     region_rows * 2 * D * ad.element_size(), full)
+                     region_total * 2 * D * ad.element_size(), full)
     else:
         got = torch.empty_like(qd)
         for f in range(frames):
             sl = slice(f * T, (f + 1) * T)
             fn = (api.attn_forward_single_frame if dtype == torch.float32
                   else api.attn_forward_single_frame_bf16)
-            fn(qd[sl], kd, vd, ad[f * region_rows:], md[f * full:(f + 1) * full], got[sl], T,
+            fn(qd[sl], kd, vd, ad[f * region_total:], md[f * full:(f + 1) * full], got[sl], T,
                D, heads, 1, f)
         torch.cuda.synchronize()
     _check(got.float().cpu(), want, dtype)
