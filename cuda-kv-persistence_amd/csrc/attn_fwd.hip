@@ -96,6 +96,7 @@ struct AttnArgs {
     int nqb;
     int layer_order;   // 1: XCD-column work order, frames longest first
     int xcd_slots;     // layer order: workgroups one XCD runs at once (0: unknown)
+    int cyclic;        // layer order: the window cuts the ranges (walk order below)
     float scale_log2;  // log2(e) / sqrt(head_dim)
 };
 
@@ -111,7 +112,8 @@ __device__ __forceinline__ int xcd_remap(int bid, int n) {
 struct WgCoord {
     int qb, split, head, frame;
     bool valid;
-    bool rev;  // visit the key tiles last to first
+    bool rev;        // visit the key tiles last to first
+    long start_key;  // >= 0: start the upward walk at the tile holding this key
 };
 
 // Number of (head, q-block) columns XCD x owns in the layer work order.
@@ -124,6 +126,7 @@ __device__ __forceinline__ WgCoord decode_wg(const AttnArgs& a) {
     c.valid = true;
     c.split = 0;
     c.rev = false;
+    c.start_key = -1;
     if (a.layer_order) {
         // Layer work order. The hardware hands workgroup b to XCD b % 8, so
         // XCD x runs workgroups x, x+8, x+16, ... in that order. XCD x owns
@@ -142,14 +145,32 @@ __device__ __forceinline__ WgCoord decode_wg(const AttnArgs& a) {
         }
         const int col = x * cols / kNumXcd + j % n;
         c.frame = a.frames - 1 - j / n;
-        // The first xcd_slots workgroups of an XCD start together and walk
-        // their keys upward from key 0 in step, so each K/V tile is fetched
-        // once for all of them. A later workgroup starts when an earlier one
-        // ends, with the long ranges still running near their top: it walks
-        // its keys downward from its range end, through the tiles the
-        // running workgroups fetched last (still in the L2), instead of
-        // restarting at key 0, whose tiles the L2 has long evicted.
-        c.rev = a.xcd_slots > 0 && j >= a.xcd_slots;
+        // Walk order, so that the workgroups an XCD runs together read the
+        // same keys at the same time (one L2 fetch for all of them):
+        // * ranges from a common first key (causal, no window): the first
+        //   xcd_slots workgroups of an XCD start together and walk upward
+        //   from that key in step. A later workgroup starts when an earlier
+        //   one ends, with the long ranges still running near their top: it
+        //   walks its keys downward from its range end, through the tiles
+        //   the running workgroups fetched last (still in the L2), instead
+        //   of restarting at the first key, whose tiles the L2 has evicted.
+        // * ranges cut by a window (every frame's range starts one frame
+        //   later than the next lower frame's): the workgroups of one round
+        //   (xcd_slots consecutive ones, started and finished together since
+        //   their ranges are equally long) all start at the first key of
+        //   the round's highest frame (its first workgroup's), walk upward
+        //   and wrap around to their own range start, so that they cross the
+        //   keys the frames share in step.
+        if (a.xcd_slots > 0) {
+            if (!a.cyclic) {
+                c.rev = j >= a.xcd_slots;
+            } else {
+                const int f_hi = a.frames - 1 - (j / a.xcd_slots) * a.xcd_slots / n;
+                const long e = a.key_end + (long)f_hi * a.kend_step;
+                const long b = e - a.max_span;
+                c.start_key = b > a.key_begin ? b : a.key_begin;
+            }
+        }
         c.head = col / a.nqb;
         c.qb = col % a.nqb;
         return c;
@@ -437,7 +458,10 @@ __device__ __forceinline__ void store_rows_staged(const AttnArgs& a, const WgCoo
 // so the L2 evicts them first and keeps the arena's lines: the counterpart of
 // the reference's access-policy window, whose misses stream
 // (src/kv_tile_manager.cu:39-47, missProp = cudaAccessPropertyStreaming).
-template <typename OutT, bool kMap, bool kColdNt>
+// kCyclic: the launch's ranges are cut by a window, and workgroups walk
+// upward from their round's start key with a wrap (decode_wg); otherwise
+// they walk upward from the range start, or downward when reversed.
+template <typename OutT, bool kMap, bool kColdNt, bool kCyclic>
 __global__ __launch_bounds__(kThreads, 2) void attn_fwd_bf16_kernel(AttnArgs a) {
     constexpr int kColdAux = kColdNt ? 2 : 0;  // buffer-load aux: bit 1 = nt
     __shared__ __attribute__((aligned(1024))) unsigned char k_lds0[kBf16TileBytes];
@@ -476,16 +500,33 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_bf16_kernel(AttnArgs a) 
     auto tile_rows_x = [&](int t, int full, int last) {
         return (unsigned)t < (unsigned)(ntiles - 1) ? full : (t == ntiles - 1 ? last : 0);
     };
-    // Key tile visited at loop step i: upward, or downward for a reversed
-    // workgroup (decode_wg); steps past the walk map outside [0, ntiles).
-    // The first key of step i's tile is computed in 64 bits from i itself
-    // (key_first + i * key_step), so that the tile addresses stay induction
-    // variables of the loop.
-    const int t_first = c.rev ? ntiles - 1 : 0;
+    // Key tile visited at loop step i (walk order: decode_wg): upward from
+    // tile 0; downward from the last tile; or upward from the tile holding
+    // start_key, wrapping to tile 0 after the last one. Steps past the walk
+    // map outside [0, ntiles). The loop carries the map-entry and byte
+    // offsets of the tiles it sets up as recurrences (one loop-invariant
+    // step, less the range's tile span at the step where the walk wraps),
+    // so that no 64-bit multiply enters the loop.
+    int t_first = c.rev ? ntiles - 1 : 0;
+    if (kCyclic && c.start_key >= kbeg && ntiles > 0) {
+        const long st = (c.start_key - kbeg) / kBf16BlockKeys;
+        t_first = st < ntiles ? (int)st : ntiles - 1;
+    }
     const int t_dir = c.rev ? -1 : 1;
-    auto tix = [&](int i) { return t_first + t_dir * i; };
+    const int wrap_at = ntiles - t_first;  // upward walks from t_first (kCyclic)
+    auto tix = [&](int i) {
+        const int t = t_first + t_dir * i;
+        if constexpr (!kCyclic) return t;
+        return i < wrap_at ? t : (i < ntiles ? t - ntiles : -1);
+    };
     const long key_first = kbeg + (long)t_first * kBf16BlockKeys;
     const long key_step = (long)t_dir * kBf16BlockKeys;
+    const long key_wrap = (long)ntiles * kBf16BlockKeys;
+    // offset of step i+1's tile from step i's (i + 1 == wrap_at: the wrap)
+    auto next_off = [&](long off, int i, long step, long wrap) {
+        if constexpr (!kCyclic) return off + step;
+        return off + step - (i + 1 == wrap_at ? wrap : 0L);
+    };
 
     const __bf16* Q = reinterpret_cast<const __bf16*>(a.q) + (long)c.frame * a.q_fstride;
     const unsigned char* Kb = reinterpret_cast<const unsigned char*>(a.k) + 2L * c.frame * a.kv_fstride;
@@ -609,13 +650,13 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_bf16_kernel(AttnArgs a) 
             md[i] = ok ? 2u * lo[i] * rb : ~0u;
         }
     };
-    // the map words of step i's tile (see above); zeros outside the range
-    auto load_map = [&](int i) -> unsigned {
+    // the map words of step i's tile, whose first key is t0 (see above);
+    // zeros outside the range
+    auto load_map = [&](int i, long t0) -> unsigned {
         if constexpr (!kMap) return ~0u;
         const int t = tix(i);
         // outside the range (at most two tiles beyond either end) the base
         // is past the slice, but the descriptor has no records to read
-        const long t0 = key_first + (long)i * key_step;
         // tiles outside the range (the loop prefetches two ahead) read zeros
         const int nrec = tile_rows_x(t, kBf16BlockKeys * 8, last_rows * 8);
         const __amdgpu_buffer_rsrc_t mrs = __builtin_amdgcn_make_buffer_rsrc(
@@ -642,11 +683,11 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_bf16_kernel(AttnArgs a) 
     unsigned pk = 0, pv = 0, pstep = 1024u;
     const unsigned sink = (unsigned)(uintptr_t)sink_lds + 2048u * (unsigned)wave;
     const unsigned lane_arena_v = lane_arena + rb;
-    auto prep_tile = [&](int i, unsigned char* kdst, unsigned char* vdst) {
+    // step i's tile starts kvo bytes into the frame's K / V
+    auto prep_tile = [&](int i, long kvo, unsigned char* kdst, unsigned char* vdst) {
         const int t = tix(i);
-        const long t0 = key_first + (long)i * key_step;
-        const unsigned char* kb = Kb + t0 * (long)rb;
-        const unsigned char* vb = Vb + t0 * (long)rb;
+        const unsigned char* kb = Kb + kvo;
+        const unsigned char* vb = Vb + kvo;
         // tiles outside the range (the loop's trailing copies) cover no rows
         const int nrec = tile_rows_x(t, kBf16BlockKeys * (int)rb, last_rows * (int)rb);
         krs = __builtin_amdgcn_make_buffer_rsrc(const_cast<unsigned char*>(kb), (short)0, nrec,
@@ -906,12 +947,20 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_bf16_kernel(AttnArgs a) 
     };
 
     unsigned hw_next = ~0u;  // map words of the tile after the next one
+    // first key of the next map load's tile, byte offset of the next
+    // prep_tile's tile
+    long map_next = next_off(key_first, 0, key_step, key_wrap);
+    const long kv_step = key_step * (long)rb;
+    const long kv_wrap = key_wrap * (long)rb;
+    long kv_next = key_first * (long)rb;
     if (ntiles > 0) {
-        const unsigned hw0 = load_map(0);
-        hw_next = load_map(1);
+        const unsigned hw0 = load_map(0, key_first);
+        hw_next = load_map(1, map_next);
+        map_next = next_off(map_next, 1, key_step, key_wrap);
         unsigned md[4] = {~0u, ~0u, ~0u, ~0u};
         decode_map(tix(0), hw0, md);
-        prep_tile(0, k_lds0, v_lds0);
+        prep_tile(0, kv_next, k_lds0, v_lds0);
+        kv_next = next_off(kv_next, 0, kv_step, kv_wrap);
 #pragma unroll
         for (int i = 0; i < 4; ++i) copy_pair(i, md);
     }
@@ -937,10 +986,12 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_bf16_kernel(AttnArgs a) 
         // (every row and map word reads as zero) and no KVMap entry is
         // decoded (rows outside the range are not entries).
         const unsigned hw1 = hw_next;
-        hw_next = load_map(t + 2);
+        hw_next = load_map(t + 2, map_next);
+        map_next = next_off(map_next, t + 2, key_step, key_wrap);
         unsigned md[4];
         decode_map(tix(t + 1), hw1, md);
-        prep_tile(t + 1, knext, vnext);
+        prep_tile(t + 1, kv_next, knext, vnext);
+        kv_next = next_off(kv_next, t + 1, kv_step, kv_wrap);
         // wave-uniform: the group mixes arena and original rows, each row's
         // source chosen per lane (copy_pair)
         const bool mixed = kMap && grp_mapped && !(kRuns && grp_run);
@@ -1389,7 +1440,7 @@ DeviceInfo device_info(int dev) {
         if (hipGetDeviceProperties(&prop, dev) == hipSuccess) di.cus = prop.multiProcessorCount;
         int nb = 0;
         if (hipOccupancyMaxActiveBlocksPerMultiprocessor(
-                &nb, attn_fwd_bf16_kernel<__bf16, true, false>, kThreads, 0) == hipSuccess &&
+                &nb, attn_fwd_bf16_kernel<__bf16, true, false, false>, kThreads, 0) == hipSuccess &&
             nb > 0)
             di.wg_per_cu_bf16 = nb;
         nb = 0;
@@ -1614,10 +1665,11 @@ int prepare_launch(const AttnLaunch& L, const DeviceInfo& di, AttnArgs& a, Launc
     a.splits = p.splits;
     a.nqb = p.nqb;
     a.layer_order = layer ? 1 : 0;
-    // Only the bf16 kernel reverses later workgroups (the fp32 kernel walks
-    // every range upward); the count assumes the occupancy the kernel was
+    // Only the bf16 kernel orders its walks (the fp32 kernel walks every
+    // range upward); the count assumes the occupancy the kernel was
     // measured at, and only steers the order, never correctness.
     a.xcd_slots = layer && L.dtype == 1 ? std::max(1, di.cus / kNumXcd) * di.wg_per_cu_bf16 : 0;
+    a.cyclic = max_key_end - L.key_begin > max_span ? 1 : 0;
     a.scale_log2 = kLog2e / sqrtf((float)kHeadDim);
     return 0;
 }
@@ -1684,14 +1736,21 @@ int launch_attention(const AttnLaunch& L) {
     }
     hipStream_t st = static_cast<hipStream_t>(L.stream);
     if (L.dtype == 1) {
+        // the non-temporal lever walks every range upward or reversed
         if (a.kvmap && L.cold_rows_nt)
-            hipLaunchKernelGGL((attn_fwd_bf16_kernel<__bf16, true, true>),
+            hipLaunchKernelGGL((attn_fwd_bf16_kernel<__bf16, true, true, false>),
+                               dim3((unsigned)p.grid), dim3(kThreads), 0, st, a);
+        else if (a.kvmap && a.cyclic)
+            hipLaunchKernelGGL((attn_fwd_bf16_kernel<__bf16, true, false, true>),
                                dim3((unsigned)p.grid), dim3(kThreads), 0, st, a);
         else if (a.kvmap)
-            hipLaunchKernelGGL((attn_fwd_bf16_kernel<__bf16, true, false>),
+            hipLaunchKernelGGL((attn_fwd_bf16_kernel<__bf16, true, false, false>),
+                               dim3((unsigned)p.grid), dim3(kThreads), 0, st, a);
+        else if (a.cyclic)
+            hipLaunchKernelGGL((attn_fwd_bf16_kernel<__bf16, false, false, true>),
                                dim3((unsigned)p.grid), dim3(kThreads), 0, st, a);
         else
-            hipLaunchKernelGGL((attn_fwd_bf16_kernel<__bf16, false, false>),
+            hipLaunchKernelGGL((attn_fwd_bf16_kernel<__bf16, false, false, false>),
                                dim3((unsigned)p.grid), dim3(kThreads), 0, st, a);
     } else {
         if (a.kvmap)
