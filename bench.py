@@ -606,11 +606,7 @@ def fp32_legs(torch, stream, api, FramePipeline, workloads, reps=50):
             a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
             a.record()
             for _ in range(reps):
-                api.attn_forward_frames(api.FP32, q, k, v, pl.layer_arena_ptr() if gated else None,
-                                        pl.layer_map_ptr() if gated else None, o, 1, T, D, H,
-                                        cross=False,
-                                        map_frame_stride=pl.layer_map_stride() if gated else 0,
-                                        stream=stream)
+                pl.layer_attention(q, k, v, o)
             b.record()
             torch.cuda.synchronize()
         am = a.elapsed_time(b) / reps
@@ -725,24 +721,17 @@ def main():
         return e0.elapsed_time(e1) / steps, wall / steps
 
     def attn_pass(c, pl, data, gated):
-        """HIP events around every layer's attention launch (the kernel the
-        pipeline runs, on its stream), with the policy's own arena regions and
-        KVMap slices as its last step left them; returns ms per layer."""
-        T, D, H, F = c.tokens, workloads.HIDDEN, workloads.HEADS, c.frames
-        arena = pl.layer_arena_ptr() if gated else None
-        kvmap = pl.layer_map_ptr() if gated else None
-        ms = pl.layer_map_stride() if gated else 0
+        """HIP events around every layer's attention launch: the pipeline's own
+        launch (kvp_pipeline_layer_attention, on its stream) with the layer
+        arena, KVMap slices and group descriptors its last run left; returns
+        ms per layer."""
         evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
                for _ in data]
         scratch = torch.empty_like(data[0][3])
         for rep in range(2):  # the first pass warms, the second is measured
             for (q, k, v, _, _), (a, b) in zip(data, evs):
                 a.record()
-                api.attn_forward_frames(api.BF16, q, k, v, arena, kvmap, scratch, F, T, D, H,
-                                        cross=True, window_frames=c.window,
-                                        map_frame_stride=ms,
-                                        cold_rows_nt=args.cold_rows_nt and gated,
-                                        stream=stream)
+                pl.layer_attention(q, k, v, scratch)
                 b.record()
             torch.cuda.synchronize()
         return sum(a.elapsed_time(b) for a, b in evs) / len(evs)

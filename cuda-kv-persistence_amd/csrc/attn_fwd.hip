@@ -70,6 +70,13 @@ struct AttnArgs {
     const void* v;
     const void* arena;
     const long* kvmap;
+    // Group descriptors (bf16 KVMap launches, optional): per frame, one
+    // 2-word entry per 16-row copy group of the frame's key range, telling
+    // which of the group's rows the map sends to the arena (format:
+    // kvp_c_api.h, kvp_attn_forward_frames_gd). With them the kernel reads
+    // map entries only for groups the entry cannot describe.
+    const unsigned* gdesc;
+    long gd_fstride;  // entries (word pairs) between frames' tables
     void* out;
     void* part_o;     // [splits][frames][nq][D] normalised partial O:
                       // fp16 from the bf16 kernel (row scaled by 2^e),
@@ -461,8 +468,12 @@ __device__ __forceinline__ void store_rows_staged(const AttnArgs& a, const WgCoo
 // kCyclic: the launch's ranges are cut by a window, and workgroups walk
 // upward from their round's start key with a wrap (decode_wg); otherwise
 // they walk upward from the range start, or downward when reversed.
-template <typename OutT, bool kMap, bool kColdNt, bool kCyclic>
+// kGd (KVMap launches with group descriptors, a.gdesc): each wave reads its
+// copy group's 8-byte descriptor per tile instead of the group's 16 map
+// entries; only groups whose descriptor says "general" read the entries.
+template <typename OutT, bool kMap, bool kColdNt, bool kCyclic, bool kGd = false>
 __global__ __launch_bounds__(kThreads, 2) void attn_fwd_bf16_kernel(AttnArgs a) {
+    static_assert(!kGd || (kMap && !kColdNt), "group descriptors serve the KVMap kernel");
     constexpr int kColdAux = kColdNt ? 2 : 0;  // buffer-load aux: bit 1 = nt
     __shared__ __attribute__((aligned(1024))) unsigned char k_lds0[kBf16TileBytes];
     __shared__ __attribute__((aligned(1024))) unsigned char v_lds0[kBf16TileBytes];
@@ -650,18 +661,54 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_bf16_kernel(AttnArgs a) 
             md[i] = ok ? 2u * lo[i] * rb : ~0u;
         }
     };
-    // the map words of step i's tile, whose first key is t0 (see above);
-    // zeros outside the range
-    auto load_map = [&](int i, long t0) -> unsigned {
+    // the map words of tile t, whose first key is t0 (see above); zeros
+    // outside the range
+    auto load_map_tile = [&](int t, long t0) -> unsigned {
         if constexpr (!kMap) return ~0u;
-        const int t = tix(i);
         // outside the range (at most two tiles beyond either end) the base
         // is past the slice, but the descriptor has no records to read
-        // tiles outside the range (the loop prefetches two ahead) read zeros
         const int nrec = tile_rows_x(t, kBf16BlockKeys * 8, last_rows * 8);
         const __amdgpu_buffer_rsrc_t mrs = __builtin_amdgcn_make_buffer_rsrc(
             const_cast<long*>(map + t0), (short)0, nrec, kBufFlags);
         return __builtin_amdgcn_raw_buffer_load_b32(mrs, 128u * wave + 4u * lane, 0, 0);
+    };
+    // the map words of step i's tile
+    auto load_map = [&](int i, long t0) -> unsigned { return load_map_tile(tix(i), t0); };
+
+    // Group descriptors (kGd): entry 4*t + w of the workgroup's table
+    // describes rows 16w..16w+15 of tile t, i.e. wave w's copy group. The
+    // table starts at the workgroup's first key (a split starts a multiple
+    // of 64 keys into its frame's range) and its descriptor covers exactly
+    // the tiles of the range, so the loop's prefetches past either end of
+    // the walk read zeros ("no arena row").
+    const unsigned* gdf =
+        kGd ? a.gdesc + 2L * c.frame * a.gd_fstride + 2L * ((long)c.split * a.keys_per_split / 16)
+            : nullptr;
+    const __amdgpu_buffer_rsrc_t gd_rs = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<unsigned*>(gdf), (short)0, kGd ? ntiles * 32 : 0, kBufFlags);
+    // step i's descriptor: even lanes load its word 0, odd lanes word 1
+    // (prep_gd takes them from lanes 0 and 1). Per-lane offsets on
+    // purpose: a load whose address the compiler sees as uniform counts as a
+    // uniform value, and the copy descriptors derived from it then end up in
+    // VGPRs, each copy wrapped in a lane-by-lane (waterfall) loop.
+    auto load_gd = [&](int i) -> unsigned {
+        if constexpr (!kGd) return 0u;
+        // a tile index below 0 wraps the offset far past the records
+        const unsigned off = (unsigned)(4 * tix(i) + wave) * 8u + 4u * (unsigned)(lane & 1);
+        return __builtin_amdgcn_raw_buffer_load_b32(gd_rs, off, 0, 0);
+    };
+    // Row rr (0..15) of the group against a sub-run word w (bit 31 set:
+    // rows r0..r0+n-1 map to arena rows l..l+n-1): the arena byte offset of
+    // the row's arena row, or `off` unchanged when the row is not in the
+    // sub-run, lies past the range end, or its arena row is beyond the reach
+    // of 32-bit offsets (such rows read the original row, as in decode_map).
+    auto sub_run = [&](unsigned w, unsigned rr, unsigned row_ok, unsigned off) -> unsigned {
+        const unsigned l = w & 0x7FFFFFu;
+        const unsigned r0 = (w >> 23) & 15u;
+        const unsigned n = ((w >> 27) & 15u) + 1u;
+        const unsigned m = l + (rr - r0);
+        const bool in = (w >> 31) != 0u && rr - r0 < n && m <= max_arena_row && row_ok != 0u;
+        return in ? 2u * m * rb : off;
     };
     // A tile's copies are set up by prep_tile (descriptors and LDS bases)
     // and issued as 4 K/V pairs. Issued back to back, a wave's 8 copies
@@ -953,62 +1000,211 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_bf16_kernel(AttnArgs a) 
     const long kv_step = key_step * (long)rb;
     const long kv_wrap = key_wrap * (long)rb;
     long kv_next = key_first * (long)rb;
-    if (ntiles > 0) {
-        const unsigned hw0 = load_map(0, key_first);
-        hw_next = load_map(1, map_next);
-        map_next = next_off(map_next, 1, key_step, key_wrap);
+
+    // ---- copies of a descriptor launch (kGd) ----
+    // Copy i of a wave moves rows 4i..4i+3 of its 16-row group (row
+    // 4i + (lane >> 4), chunk lane & 15, as in copy_plain) as structured
+    // buffer loads: record index = the row in the group, stride = the source's
+    // row pitch. Original rows (pitch rb, descriptor based at the group's
+    // first row) and arena rows ([K row | V row], pitch 2 rb) then take the
+    // same per-lane operands, and the scalar descriptor alone picks the
+    // source of each copy. Rows at or past the range end are records past
+    // the descriptor's count and read as zeros.
+    unsigned gvidx[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) gvidx[i] = (unsigned)(4 * i + (lane >> 4));
+    // the step being set up (prep_gd): its original rows, the arena sub-run
+    // its copies may take, which of the 4 copies take it, and what the slow
+    // path needs
+    const unsigned char* go_k = Kb;
+    const unsigned char* go_v = Vb;
+    int go_n = 0;                     // rows of the group inside the range
+    const unsigned char* ga_k = Ab;   // K part of arena row (l - r0) of the sub-run
+    unsigned gsel = 0;                // bit i: copy i reads the sub-run
+    bool gslow = false;               // some rows need a per-row source
+    unsigned gw0 = 0, gw1 = 0;        // the descriptor words (slow path)
+    int gt = 0;                       // the step's tile
+    long gkey0 = 0;                   // its first key (slow path: map words)
+    unsigned gkoff = 0, gvoff = 0;    // LDS bases of the wave's copies
+    // Step i's group of tile t (first key key0, K/V byte offset kvo) from its
+    // descriptor g (decoded from lanes 0 and 1), copies into kdst / vdst. The
+    // fast form: no arena row, or one sub-run whose rows start and end on
+    // 4-row copy boundaries (every policy tile of the frame pipeline's layer
+    // arena, whose frames start on 4-row boundaries); anything else copies
+    // the original rows and fixes the mapped ones up afterwards (overwrite_gd).
+    // Every value is a select, not assigned under a branch: branch-assigned,
+    // the compiler takes such values for divergent, moves the descriptors
+    // built from them into VGPRs and wraps every copy in a lane-by-lane loop.
+    auto prep_gd = [&](int t, long kvo, long key0, unsigned char* kdst, unsigned char* vdst,
+                       unsigned g) {
+        const unsigned w0 = (unsigned)__builtin_amdgcn_readlane((int)g, 0);
+        const unsigned w1 = (unsigned)__builtin_amdgcn_readlane((int)g, 1);
+        const int rows = tile_rows_x(t, kBf16BlockKeys, last_rows) - 16 * wave;
+        const int grows = rows < 0 ? 0 : (rows > 16 ? 16 : rows);
+        const long goff = kvo + 16L * wave * (long)rb;
+        go_k = Kb + goff;
+        go_v = Vb + goff;
+        go_n = grows;
+        const unsigned l = w0 & 0x7FFFFFu;
+        const unsigned r0 = (w0 >> 23) & 15u;
+        const unsigned n = ((w0 >> 27) & 15u) + 1u;
+        const bool fast = (w0 >> 31) != 0u && w1 == 0u && ((r0 | n) & 3u) == 0u &&
+                          (int)(r0 + n) <= grows && l + n - 1u <= max_arena_row;
+        gsel = fast ? ((1u << (n >> 2)) - 1u) << (r0 >> 2) : 0u;
+        ga_k = Ab + 2L * (long)rb * ((long)l - (long)r0);
+        gslow = w0 != 0u && !fast;
+        gw0 = w0;
+        gw1 = w1;
+        gt = t;
+        gkey0 = key0;
+        gkoff = (unsigned)__builtin_amdgcn_readfirstlane((int)(uintptr_t)kdst) + 4096u * wave;
+        gvoff = (unsigned)__builtin_amdgcn_readfirstlane((int)(uintptr_t)vdst) + 4096u * wave;
+    };
+    auto copy_gd = [&](int i) {
+        const bool ar = ((gsel >> i) & 1u) != 0u;
+        const short pitch = (short)(ar ? 2u * rb : rb);
+        const int nrec = ar ? 16 : go_n;
+        const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<unsigned char*>(ar ? ga_k : go_k), pitch, nrec, kBufFlags);
+        const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<unsigned char*>(ar ? ga_k + rb : go_v), pitch, nrec, kBufFlags);
+        KVP_LDS void* kd = (KVP_LDS void*)(uintptr_t)(gkoff + 1024u * (unsigned)i);
+        KVP_LDS void* vd = (KVP_LDS void*)(uintptr_t)(gvoff + 1024u * (unsigned)i);
+        __builtin_amdgcn_struct_ptr_buffer_load_lds(rk, kd, 16, gvidx[i], kofs[i], 0, 0, 0);
+        __builtin_amdgcn_struct_ptr_buffer_load_lds(rv, vd, 16, gvidx[i], vofs, 0, 0, 0);
+    };
+    // The slow path of the step prep_gd set up last, after its 4 copies were
+    // issued: each row the map sends to the arena is copied again from its
+    // arena row into the same LDS row. A wave's loads complete in issue
+    // order, so the arena row lands last. Sources: the sub-run words, or for
+    // a general group the tile's map words (loaded now).
+    auto overwrite_gd = [&]() {
+        if (__builtin_expect(!gslow, 1)) return;
         unsigned md[4] = {~0u, ~0u, ~0u, ~0u};
-        decode_map(tix(0), hw0, md);
-        prep_tile(0, kv_next, k_lds0, v_lds0);
-        kv_next = next_off(kv_next, 0, kv_step, kv_wrap);
+        if (gw0 == 1u) {
+            decode_map(gt, load_map_tile(gt, gkey0), md);
+        } else {
+            const int valid_rows = tile_rows_x(gt, kBf16BlockKeys, last_rows);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) copy_pair(i, md);
-    }
-    // Compiler-visible wait for every load so far (Q, map, tile 0): the loop
-    // then never waits for vector memory on the Q registers' account.
-    __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
-    for (int t = 0; t < ntiles; ++t) {
-        // t counts loop steps; step t computes tile tix(t). Step t's tile
-        // lives in stage t & 1; step t+1's tile streams into the other stage,
-        // which held step t-1's: every wave finished reading it before it
-        // reached the barrier below, so one barrier per tile suffices
-        unsigned char* kcur = (t & 1) ? k_lds1 : k_lds0;
-        unsigned char* vcur = (t & 1) ? v_lds1 : v_lds0;
-        unsigned char* knext = (t & 1) ? k_lds0 : k_lds1;
-        unsigned char* vnext = (t & 1) ? v_lds0 : v_lds1;
-        // each wave's copies of step t's tile (and its map load) have
-        // landed, then the barrier publishes the whole tile
-        wait_vm<0>();
-        wg_barrier();
-        // The copies for step t+1 and the map load for step t+2 are issued
-        // unconditionally, so the QK k-steps they sit between stay one basic
-        // block: past the end of the walk the descriptors cover no rows
-        // (every row and map word reads as zero) and no KVMap entry is
-        // decoded (rows outside the range are not entries).
-        const unsigned hw1 = hw_next;
-        hw_next = load_map(t + 2, map_next);
-        map_next = next_off(map_next, t + 2, key_step, key_wrap);
-        unsigned md[4];
-        decode_map(tix(t + 1), hw1, md);
-        prep_tile(t + 1, kv_next, knext, vnext);
-        kv_next = next_off(kv_next, t + 1, kv_step, kv_wrap);
-        // wave-uniform: the group mixes arena and original rows, each row's
-        // source chosen per lane (copy_pair)
-        const bool mixed = kMap && grp_mapped && !(kRuns && grp_run);
-        if (active) {
-            if (__builtin_expect(mixed, 0)) {
-#pragma unroll
-                for (int i = 0; i < 4; ++i) copy_pair(i, md);
+            for (int i = 0; i < 4; ++i) {
+                const unsigned rr = (unsigned)((lane >> 4) + 4 * i);
+                const unsigned ok = ld_row0 + 4 * i < valid_rows ? 1u : 0u;
+                md[i] = sub_run(gw1, rr, ok, sub_run(gw0, rr, ok, ~0u));
             }
-            compute_tile(tix(t), kcur, vcur, [&](int ks) {
-                if ((ks & 1) == 0) copy_plain(ks >> 1);
-            });
-        } else if (mixed) {
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            if (md[i] != ~0u) {
+                KVP_LDS void* kd = (KVP_LDS void*)(uintptr_t)(gkoff + 1024u * (unsigned)i);
+                KVP_LDS void* vd = (KVP_LDS void*)(uintptr_t)(gvoff + 1024u * (unsigned)i);
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(arena_rs, kd, 16, md[i] + kofs[i], 0, 0, 0);
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(arena_rs, vd, 16, md[i] + rb + vofs, 0, 0,
+                                                         0);
+            }
+        }
+    };
+
+    if constexpr (kGd) {
+        // Step t+2 is set up at the end of step t (after its MFMAs, where the
+        // wave would otherwise wait at the next barrier): its descriptor,
+        // loaded one step earlier, its copy parameters (into the stage step t
+        // read; the copies are issued after the barrier) and the load of step
+        // t+3's descriptor.
+        unsigned gd_next = 0u;
+        long gd_key = key_first;
+        if (ntiles > 0) {
+            const unsigned g0 = load_gd(0);
+            const unsigned g1 = load_gd(1);
+            prep_gd(tix(0), kv_next, gd_key, k_lds0, v_lds0, g0);
+            kv_next = next_off(kv_next, 0, kv_step, kv_wrap);
+            gd_key = next_off(gd_key, 0, key_step, key_wrap);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) copy_gd(i);
+            overwrite_gd();
+            prep_gd(tix(1), kv_next, gd_key, k_lds1, v_lds1, g1);
+            kv_next = next_off(kv_next, 1, kv_step, kv_wrap);
+            gd_key = next_off(gd_key, 1, key_step, key_wrap);
+            gd_next = load_gd(2);
+        }
+        __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
+        for (int t = 0; t < ntiles; ++t) {
+            unsigned char* kcur = (t & 1) ? k_lds1 : k_lds0;
+            unsigned char* vcur = (t & 1) ? v_lds1 : v_lds0;
+            wait_vm<0>();
+            wg_barrier();
+            if (active) {
+                compute_tile(tix(t), kcur, vcur, [&](int ks) {
+                    if ((ks & 1) == 0) copy_gd(ks >> 1);
+                });
+            } else {
+#pragma unroll
+                for (int i = 0; i < 4; ++i) copy_gd(i);
+            }
+            overwrite_gd();
+            prep_gd(tix(t + 2), kv_next, gd_key, kcur, vcur, gd_next);
+            kv_next = next_off(kv_next, t + 2, kv_step, kv_wrap);
+            gd_key = next_off(gd_key, t + 2, key_step, key_wrap);
+            gd_next = load_gd(t + 3);
+        }
+    } else {
+        if (ntiles > 0) {
+            const unsigned hw0 = load_map(0, key_first);
+            hw_next = load_map(1, map_next);
+            map_next = next_off(map_next, 1, key_step, key_wrap);
+            unsigned md[4] = {~0u, ~0u, ~0u, ~0u};
+            decode_map(tix(0), hw0, md);
+            prep_tile(0, kv_next, k_lds0, v_lds0);
+            kv_next = next_off(kv_next, 0, kv_step, kv_wrap);
 #pragma unroll
             for (int i = 0; i < 4; ++i) copy_pair(i, md);
-        } else {
+        }
+        // Compiler-visible wait for every load so far (Q, map, tile 0): the
+        // loop then never waits for vector memory on the Q registers' account.
+        __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
+        for (int t = 0; t < ntiles; ++t) {
+            // t counts loop steps; step t computes tile tix(t). Step t's tile
+            // lives in stage t & 1; step t+1's tile streams into the other
+            // stage, which held step t-1's: every wave finished reading it
+            // before it reached the barrier below, so one barrier per tile
+            // suffices
+            unsigned char* kcur = (t & 1) ? k_lds1 : k_lds0;
+            unsigned char* vcur = (t & 1) ? v_lds1 : v_lds0;
+            unsigned char* knext = (t & 1) ? k_lds0 : k_lds1;
+            unsigned char* vnext = (t & 1) ? v_lds0 : v_lds1;
+            // each wave's copies of step t's tile (and its map load) have
+            // landed, then the barrier publishes the whole tile
+            wait_vm<0>();
+            wg_barrier();
+            // The copies for step t+1 and the map load for step t+2 are issued
+            // unconditionally, so the QK k-steps they sit between stay one
+            // basic block: past the end of the walk the descriptors cover no
+            // rows (every row and map word reads as zero) and no KVMap entry
+            // is decoded (rows outside the range are not entries).
+            const unsigned hw1 = hw_next;
+            hw_next = load_map(t + 2, map_next);
+            map_next = next_off(map_next, t + 2, key_step, key_wrap);
+            unsigned md[4];
+            decode_map(tix(t + 1), hw1, md);
+            prep_tile(t + 1, kv_next, knext, vnext);
+            kv_next = next_off(kv_next, t + 1, kv_step, kv_wrap);
+            // wave-uniform: the group mixes arena and original rows, each
+            // row's source chosen per lane (copy_pair)
+            const bool mixed = kMap && grp_mapped && !(kRuns && grp_run);
+            if (active) {
+                if (__builtin_expect(mixed, 0)) {
 #pragma unroll
-            for (int i = 0; i < 4; ++i) copy_plain(i);
+                    for (int i = 0; i < 4; ++i) copy_pair(i, md);
+                }
+                compute_tile(tix(t), kcur, vcur, [&](int ks) {
+                    if ((ks & 1) == 0) copy_plain(ks >> 1);
+                });
+            } else if (mixed) {
+#pragma unroll
+                for (int i = 0; i < 4; ++i) copy_pair(i, md);
+            } else {
+#pragma unroll
+                for (int i = 0; i < 4; ++i) copy_plain(i);
+            }
         }
     }
     // the trailing copies land before the workgroup's LDS is released, and
@@ -1602,6 +1798,18 @@ int validate_launch(const AttnLaunch& L) {
         set_error("attention: kvmap given without arena");
         return 1;
     }
+    if (L.gdesc && (!L.kvmap || L.dtype != 1 || L.cold_rows_nt || L.gd_fstride < 0 ||
+                    (uintptr_t)L.gdesc % 8)) {
+        set_error("attention: group descriptors need a bf16 KVMap launch without the "
+                  "non-temporal lever, an 8-byte aligned table and a non-negative stride");
+        return 1;
+    }
+    // the descriptor kernel reads arena rows with a record pitch of 2 * row
+    // bytes = 4 * D, which a buffer descriptor's 14-bit stride field must hold
+    if (L.gdesc && 4L * L.D > 16383) {
+        set_error("attention: group descriptors need D <= 4095 (D=%d)", L.D);
+        return 1;
+    }
     if (L.arena_fstride % 16) {
         set_error("attention: arena regions must be 16-byte aligned");
         return 1;
@@ -1639,12 +1847,22 @@ int prepare_launch(const AttnLaunch& L, const DeviceInfo& di, AttnArgs& a, Launc
         set_error("attention: grid too large");
         return 1;
     }
+    // every frame's table (gd_fstride entries, also for one frame) covers
+    // the 16-row groups of the longest range
+    if (L.gdesc &&
+        L.gd_fstride < 4 * ((span_last + kBf16BlockKeys - 1) / kBf16BlockKeys)) {
+        set_error("attention: group-descriptor stride %ld below the %ld groups of a range",
+                  L.gd_fstride, 4 * ((span_last + kBf16BlockKeys - 1) / kBf16BlockKeys));
+        return 1;
+    }
 
     a.q = L.q;
     a.k = L.k;
     a.v = L.v;
     a.arena = L.arena;
     a.kvmap = L.kvmap;
+    a.gdesc = L.gdesc;
+    a.gd_fstride = L.gd_fstride;
     a.out = L.out;
     a.part_o = nullptr;
     a.part_lse = nullptr;
@@ -1739,6 +1957,12 @@ int launch_attention(const AttnLaunch& L) {
         // the non-temporal lever walks every range upward or reversed
         if (a.kvmap && L.cold_rows_nt)
             hipLaunchKernelGGL((attn_fwd_bf16_kernel<__bf16, true, true, false>),
+                               dim3((unsigned)p.grid), dim3(kThreads), 0, st, a);
+        else if (a.gdesc && a.cyclic)
+            hipLaunchKernelGGL((attn_fwd_bf16_kernel<__bf16, true, false, true, true>),
+                               dim3((unsigned)p.grid), dim3(kThreads), 0, st, a);
+        else if (a.gdesc)
+            hipLaunchKernelGGL((attn_fwd_bf16_kernel<__bf16, true, false, false, true>),
                                dim3((unsigned)p.grid), dim3(kThreads), 0, st, a);
         else if (a.kvmap && a.cyclic)
             hipLaunchKernelGGL((attn_fwd_bf16_kernel<__bf16, true, false, true>),

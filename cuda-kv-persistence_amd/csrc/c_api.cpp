@@ -12,6 +12,7 @@
 #include "attn_kernel.h"
 #include "kv_tile_manager.h"
 #include "kvp_c_api.h"
+#include "group_desc.h"
 #include "kvp_internal.h"
 #include "tile_gating_policy.h"
 #include "tile_layout.h"
@@ -228,10 +229,14 @@ int kvp_attn_forward_range_noalloc(int dtype, const void* q, const void* k, cons
     return kvp::launch_attention_noalloc(L);
 }
 
-int kvp_attn_forward_frames(int dtype, const void* q, const void* k, const void* v,
-                            const void* arena, long arena_frame_bytes, const long* kvmap,
-                            long map_frame_stride, void* out, int frames, int T, int D,
-                            int heads, int cross, int window_frames, int flags, void* stream) {
+}  // extern "C"
+
+// A layer launch of kvp_attn_forward_frames(_gd).
+static int forward_frames(int dtype, const void* q, const void* k, const void* v,
+                          const void* arena, long arena_frame_bytes, const long* kvmap,
+                          long map_frame_stride, const unsigned* gdesc, long gd_frame_stride,
+                          void* out, int frames, int T, int D, int heads, int cross,
+                          int window_frames, int flags, void* stream) {
     if (T <= 0 || frames <= 0 || window_frames < 0 || arena_frame_bytes < 0 ||
         map_frame_stride < 0) {
         kvp::set_error("attention: bad layer arguments (T=%d frames=%d window=%d)", T, frames,
@@ -239,6 +244,8 @@ int kvp_attn_forward_frames(int dtype, const void* q, const void* k, const void*
         return 1;
     }
     kvp::AttnLaunch L;
+    L.gdesc = gdesc;
+    L.gd_fstride = gd_frame_stride;
     L.dtype = dtype;
     L.q = q;
     L.k = k;
@@ -265,6 +272,67 @@ int kvp_attn_forward_frames(int dtype, const void* q, const void* k, const void*
         L.kv_fstride = (long)T * D;
     }
     return kvp::launch_attention(L);
+}
+
+extern "C" {
+
+int kvp_attn_forward_frames(int dtype, const void* q, const void* k, const void* v,
+                            const void* arena, long arena_frame_bytes, const long* kvmap,
+                            long map_frame_stride, void* out, int frames, int T, int D,
+                            int heads, int cross, int window_frames, int flags, void* stream) {
+    return forward_frames(dtype, q, k, v, arena, arena_frame_bytes, kvmap, map_frame_stride,
+                          nullptr, 0, out, frames, T, D, heads, cross, window_frames, flags,
+                          stream);
+}
+
+int kvp_attn_forward_frames_gd(const void* q, const void* k, const void* v, const void* arena,
+                               long arena_frame_bytes, const long* kvmap, long map_frame_stride,
+                               const unsigned* gdesc, long gd_frame_stride, void* out,
+                               int frames, int T, int D, int heads, int cross, int window_frames,
+                               void* stream) {
+    if (!gdesc) {
+        kvp::set_error("attention: null group-descriptor table");
+        return 1;
+    }
+    return forward_frames(1, q, k, v, arena, arena_frame_bytes, kvmap, map_frame_stride, gdesc,
+                          gd_frame_stride, out, frames, T, D, heads, cross, window_frames, 0,
+                          stream);
+}
+
+long kvp_attn_group_desc(const long* map, long key_begin, long key_end, int D, unsigned* out,
+                         long cap) {
+    if (!map || key_begin < 0 || key_end <= key_begin || D <= 0 || cap < 0 ||
+        (cap > 0 && !out)) {
+        kvp::set_error("group descriptors: bad arguments");
+        return -1;
+    }
+    const long n = 4 * ((key_end - key_begin + 63) / 64);
+    if (cap < n) return n;
+    // an entry counts when its arena row lies within the bf16 kernel's
+    // 32-bit reach: 2 * (m + 1) * (2 * D) <= 2^32
+    const long max_row = 0x80000000L / (2L * D) - 1;
+    std::vector<kvp::gd::Sub> subs;
+    for (long j = key_begin; j < key_end;) {
+        const long m = map[j];
+        if (m < 0 || m > max_row) {
+            ++j;
+            continue;
+        }
+        long r = 1;
+        while (j + r < key_end && map[j + r] == m + r && m + r <= max_row &&
+               (j + r - key_begin) % 16 != 0)
+            ++r;
+        kvp::gd::add_rows(subs, j, r, m, key_begin, key_end);
+        j += r;
+    }
+    std::vector<kvp::gd::Ent> ents;
+    kvp::gd::encode(subs, ents);
+    std::fill(out, out + 2 * n, 0u);
+    for (const kvp::gd::Ent& e : ents) {
+        out[2 * e.g] = e.w0;
+        out[2 * e.g + 1] = e.w1;
+    }
+    return n;
 }
 
 }  // extern "C"

@@ -27,6 +27,7 @@
 
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <climits>
 #include <cstdarg>
 #include <cstdint>
@@ -109,8 +110,9 @@ __global__ __launch_bounds__(stage::kRunThreads) void stage_runs_kernel(const Ru
     stage::stage_runs_block(a, (int)blockIdx.x);
 }
 
-// Layer staging: workgroups [0, n_copies) copy one run each, the ones after
-// that write one KVMap run each. A copy run moves n arena rows of
+// Layer staging: workgroups [0, n_copies) copy one run each, the next
+// n_map_runs write one KVMap run each, the ones after that write 256
+// group-descriptor entries each. A copy run moves n arena rows of
 // 2 * cpr 16-byte chunks; chunk w < cpr of a row comes from its K row, the
 // rest from its V row. Each thread keeps four chunks in flight before it
 // stores them.
@@ -119,9 +121,10 @@ constexpr int kLayerBatch = 4;
 
 __global__ __launch_bounds__(kLayerThreads) void layer_stage_kernel(
     const LayerCopyRun* __restrict__ copies, long n_copies,
-    const LayerMapRun* __restrict__ map_runs, unsigned char* __restrict__ arena,
+    const LayerMapRun* __restrict__ map_runs, long n_map_runs,
+    const LayerGdWrite* __restrict__ gd_writes, long n_gd, unsigned char* __restrict__ arena,
     const unsigned char* __restrict__ k, const unsigned char* __restrict__ v, unsigned cpr,
-    long* __restrict__ map) {
+    long* __restrict__ map, unsigned* __restrict__ gd) {
     typedef __attribute__((ext_vector_type(4))) unsigned int u32x4;
     const long b = blockIdx.x;
     if (b < n_copies) {
@@ -150,11 +153,24 @@ __global__ __launch_bounds__(kLayerThreads) void layer_stage_kernel(
             for (int u = 0; u < kLayerBatch; ++u)
                 if (dst[u]) *reinterpret_cast<u32x4*>(dst[u]) = val[u];
         }
-    } else {
+    } else if (b < n_copies + n_map_runs) {
         const LayerMapRun m = map_runs[b - n_copies];
         for (int j = (int)threadIdx.x; j < m.n; j += kLayerThreads)
             map[m.index + j] = m.value < 0 ? -1L : (long)m.value + j;
+    } else {
+        const long i = (b - n_copies - n_map_runs) * kLayerThreads + threadIdx.x;
+        if (i < n_gd) {
+            const LayerGdWrite w = gd_writes[i];
+            typedef __attribute__((ext_vector_type(2))) unsigned int u32x2;
+            *reinterpret_cast<u32x2*>(gd + 2 * w.index) = u32x2{w.w0, w.w1};
+        }
     }
+}
+
+__global__ __launch_bounds__(256) void fill_words_kernel(unsigned* __restrict__ dst, long n,
+                                                         unsigned value) {
+    for (long i = (long)blockIdx.x * 256 + threadIdx.x; i < n; i += (long)gridDim.x * 256)
+        dst[i] = value;
 }
 
 // Descriptor ring in mapped, coherent host memory: the host writes a
@@ -471,19 +487,39 @@ int stage_plan_launch(const void* plan, void* stream) {
 
 void stage_plan_free(void* plan) { delete static_cast<StagePlan*>(plan); }
 
+int fill_words(void* dst, long n, unsigned value, void* stream) {
+    if (n <= 0) return 0;
+    if (!dst) {
+        set_error("fill: null destination");
+        return 1;
+    }
+    const long blocks = std::min<long>((n + 255) / 256, 4096);
+    hipLaunchKernelGGL(fill_words_kernel, dim3((unsigned)blocks), dim3(256), 0,
+                       static_cast<hipStream_t>(stream), static_cast<unsigned*>(dst), n, value);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) {
+        set_error("fill launch: %s", hipGetErrorString(e));
+        return 1;
+    }
+    return 0;
+}
+
 int layer_stage_launch(void* stager, void* arena, const void* k, const void* v, long row_bytes,
                        const LayerCopyRun* copies, long n_copies, long* map,
-                       const LayerMapRun* map_runs, long n_map_runs, void* stream) {
+                       const LayerMapRun* map_runs, long n_map_runs, unsigned* gd,
+                       const LayerGdWrite* gd_writes, long n_gd_writes, void* stream) {
     Stager* st = static_cast<Stager*>(stager);
     if (!st) {
         set_error("layer stage: null stager");
         return 1;
     }
-    if (n_copies < 0 || n_map_runs < 0 || n_copies + n_map_runs > INT_MAX) {
+    const long gd_blocks = (n_gd_writes + kLayerThreads - 1) / kLayerThreads;
+    if (n_copies < 0 || n_map_runs < 0 || n_gd_writes < 0 ||
+        n_copies + n_map_runs + gd_blocks > INT_MAX) {
         set_error("layer stage: bad run counts");
         return 1;
     }
-    if (n_copies + n_map_runs == 0) return 0;
+    if (n_copies + n_map_runs + gd_blocks == 0) return 0;
     if (n_copies > 0 && (!arena || !k || !v || row_bytes <= 0 || row_bytes % 16 ||
                          ((uintptr_t)arena | (uintptr_t)k | (uintptr_t)v) % 16)) {
         set_error("layer stage: copies need 16-byte aligned arena, K, V and row size");
@@ -493,8 +529,13 @@ int layer_stage_launch(void* stager, void* arena, const void* k, const void* v, 
         set_error("layer stage: map runs without a map");
         return 1;
     }
+    if (n_gd_writes > 0 && (!gd || (uintptr_t)gd % 8)) {
+        set_error("layer stage: descriptor writes need an 8-byte aligned table");
+        return 1;
+    }
     const size_t copy_bytes = align256((size_t)n_copies * sizeof(LayerCopyRun));
-    const size_t need = copy_bytes + align256((size_t)n_map_runs * sizeof(LayerMapRun));
+    const size_t map_bytes = align256((size_t)n_map_runs * sizeof(LayerMapRun));
+    const size_t need = copy_bytes + map_bytes + align256((size_t)n_gd_writes * sizeof(LayerGdWrite));
     hipStream_t hs = static_cast<hipStream_t>(stream);
     if (!st->before_launch(hs) || !st->reserve(need)) {
         set_error("layer stage: descriptor ring allocation failed");
@@ -504,11 +545,15 @@ int layer_stage_launch(void* stager, void* arena, const void* k, const void* v, 
     unsigned char* d = st->dev + st->head;
     if (n_copies > 0) memcpy(h, copies, (size_t)n_copies * sizeof(LayerCopyRun));
     if (n_map_runs > 0) memcpy(h + copy_bytes, map_runs, (size_t)n_map_runs * sizeof(LayerMapRun));
-    hipLaunchKernelGGL(layer_stage_kernel, dim3((unsigned)(n_copies + n_map_runs)),
+    if (n_gd_writes > 0)
+        memcpy(h + copy_bytes + map_bytes, gd_writes, (size_t)n_gd_writes * sizeof(LayerGdWrite));
+    hipLaunchKernelGGL(layer_stage_kernel, dim3((unsigned)(n_copies + n_map_runs + gd_blocks)),
                        dim3(kLayerThreads), 0, hs, reinterpret_cast<const LayerCopyRun*>(d),
-                       n_copies, reinterpret_cast<const LayerMapRun*>(d + copy_bytes),
-                       static_cast<unsigned char*>(arena), static_cast<const unsigned char*>(k),
-                       static_cast<const unsigned char*>(v), (unsigned)(row_bytes / 16), map);
+                       n_copies, reinterpret_cast<const LayerMapRun*>(d + copy_bytes), n_map_runs,
+                       reinterpret_cast<const LayerGdWrite*>(d + copy_bytes + map_bytes),
+                       n_gd_writes, static_cast<unsigned char*>(arena),
+                       static_cast<const unsigned char*>(k), static_cast<const unsigned char*>(v),
+                       (unsigned)(row_bytes / 16), map, gd);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) {
         set_error("layer stage launch: %s", hipGetErrorString(e));

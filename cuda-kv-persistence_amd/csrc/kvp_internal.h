@@ -34,6 +34,10 @@ struct AttnLaunch {
     const void* v = nullptr;
     const void* arena = nullptr;
     const long* kvmap = nullptr;
+    // bf16 KVMap launches: optional group descriptors of the map (format:
+    // kvp_attn_forward_frames_gd), gd_fstride entries per frame
+    const unsigned* gdesc = nullptr;
+    long gd_fstride = 0;
     void* out = nullptr;
     int nq = 0, D = 0, heads = 0, frames = 1;
     long q_fstride = 0, kv_fstride = 0, map_fstride = 0, arena_fstride = 0;
@@ -90,12 +94,21 @@ struct LayerMapRun {
     int value;    // -1: n entries reset to -1; else entry j = value + j
     int n;        // entries, 1..kLayerMapEntries
 };
+// One entry of a group-descriptor table (2 words per entry).
+struct LayerGdWrite {
+    long index;   // entry index
+    unsigned w0, w1;
+};
 // The caller has checked every run against its buffers: src rows below
-// the K/V row count, dst rows below the arena's, map entries below the map's.
+// the K/V row count, dst rows below the arena's, map entries below the map's,
+// descriptor entries below the table's.
 // row_bytes: bytes of one K (or V) row, a multiple of 16.
 int layer_stage_launch(void* stager, void* arena, const void* k, const void* v, long row_bytes,
                        const LayerCopyRun* copies, long n_copies, long* map,
-                       const LayerMapRun* map_runs, long n_map_runs, void* stream);
+                       const LayerMapRun* map_runs, long n_map_runs, unsigned* gd,
+                       const LayerGdWrite* gd_writes, long n_gd_writes, void* stream);
+// n 32-bit words at dst set to value, on the stream (a kernel, no memset node).
+int fill_words(void* dst, long n, unsigned value, void* stream);
 
 // Grouped bf16 projection GEMM (proj_gemm.hip): for g < groups (1..3),
 // outs[g][r, n] = sum_k x[r, k] w[g*Ng + n, k] + bias[g*Ng + n]

@@ -42,6 +42,7 @@
 #include <string>
 #include <vector>
 
+#include "group_desc.h"
 #include "kv_tile_manager.h"
 #include "kvp_c_api.h"
 #include "kvp_internal.h"
@@ -101,7 +102,17 @@ struct Pipeline {
     int seg_gen = 0;
     std::vector<long> tile_phys;               // gsrc -> first physical row this run
     std::vector<int> tile_gen;                 // run that last mapped the tile
+    std::vector<int> tile_rows;                // gsrc -> longest prefix any frame maps
     int layer_gen = 0;
+    // group descriptors of the layer map (bf16): frames tables of gd_stride
+    // entries; per frame, the non-empty entries the device holds
+    unsigned* layer_gd = nullptr;
+    long gd_stride = 0;
+    std::vector<std::vector<kvp::gd::Ent>> gd_dev;
+    std::vector<kvp::gd::Sub> gd_subs;
+    std::vector<kvp::gd::Ent> gd_new;
+    std::vector<kvp::LayerGdWrite> gd_writes;
+    std::vector<unsigned> plan_gd;             // plan-only: the tables on the host
     long layer_nphys = 0;                      // physical rows assigned this run
     std::vector<long> tile_slots;              // slots of one tile (host map)
     std::vector<kvp::LayerCopyRun> layer_copies;
@@ -121,6 +132,7 @@ struct Pipeline {
         if (d_map) kvp_dev_free(d_map);
         if (layer_arena) kvp_dev_free(layer_arena);
         if (layer_map) kvp_dev_free(layer_map);
+        if (layer_gd) kvp_dev_free(layer_gd);
     }
 };
 
@@ -353,9 +365,55 @@ int step_frame(Pipeline& p, int f, const char* q, const char* k, const char* v, 
     return 0;
 }
 
-// Layer-mode state, created at the first kvp_pipeline_run: the bookkeeping
-// manager and tile tables, and (unless plan-only) the device arena, map and
-// stager.
+// Key range [b, e) of frame f in the layer launch, in key-index space (the
+// absolute key rows in cross mode, frame-relative rows in intra mode).
+void frame_range(const Pipeline& p, int f, long& b, long& e) {
+    if (p.cross) {
+        e = (long)(f + 1) * p.T;
+        b = window_first_frame(p, f) * p.T;
+    } else {
+        b = 0;
+        e = p.T;
+    }
+}
+
+// Frees the layer-mode state (device buffers after draining the stream, the
+// bookkeeping manager and every host mirror of device content). The next
+// run builds it again from scratch: after a failed run the device map and
+// descriptor tables may not match their host mirrors any more.
+void layer_teardown(Pipeline& p) {
+    if (p.layer_arena || p.layer_map || p.layer_gd || p.layer_stager) (void)kvp_stream_sync(p.stream);
+    if (p.layer_stager) kvp_stager_destroy(p.layer_stager);
+    if (p.layer_arena) kvp_dev_free(p.layer_arena);
+    if (p.layer_map) kvp_dev_free(p.layer_map);
+    if (p.layer_gd) kvp_dev_free(p.layer_gd);
+    p.layer_stager = nullptr;
+    p.layer_arena = nullptr;
+    p.layer_map = nullptr;
+    p.layer_gd = nullptr;
+    p.layer_mgr.reset();
+    if (p.last_mgr != p.mgr.get()) p.last_mgr = nullptr;
+    p.layer_cap = 0;
+    p.layer_nphys = 0;
+    p.gd_stride = 0;
+    p.frame_segs.clear();
+    p.seg_n.clear();
+    p.seg_phys.clear();
+    p.seg_list.clear();
+    p.seg_mark.clear();
+    p.tile_phys.clear();
+    p.tile_gen.clear();
+    p.tile_rows.clear();
+    p.gd_dev.clear();
+    p.plan_map.clear();
+    p.plan_stamp.clear();
+    p.plan_gd.clear();
+}
+
+// Layer-mode state, created at the first kvp_pipeline_run (and again after
+// a failed run): the bookkeeping manager and tile tables, and (unless
+// plan-only) the device arena, map, descriptor tables and stager. All or
+// nothing: on any failure everything created here is released again.
 int layer_setup(Pipeline& p) {
     if (p.layer_mgr) return 0;
     const long row_bytes = (long)p.D * p.elem;
@@ -363,19 +421,25 @@ int layer_setup(Pipeline& p) {
     p.layer_mgr.reset(new (std::nothrow) KVTileManager((size_t)p.set_aside, (size_t)p.set_aside));
     if (!p.layer_mgr || !p.layer_mgr->init() ||
         !p.layer_mgr->arena_attach(nullptr, (size_t)p.set_aside, stride_floats)) {
-        p.layer_mgr.reset();
+        layer_teardown(p);
         kvp::set_error("pipeline: layer manager init failed");
         return 1;
     }
-    // A frame maps at most region_rows rows (the budget / slot capacity);
-    // physical rows are handed out a whole tile at a time, so one frame
-    // usually adds at most region_rows + tile_tokens of them. The arena grows
-    // in the rare layer that needs more (never past frames * T rows).
+    // A frame maps at most region_rows rows (the budget / slot capacity), as
+    // a prefix of each tile it maps. The layer arena gives every tile the
+    // longest prefix any frame of the layer maps, so it never holds more
+    // than frames * region_rows rows: the reference's per-step arena summed
+    // over the layer's frames (frames * set_aside bytes).
     p.region_rows = p.set_aside / (2 * row_bytes);
-    p.layer_cap = std::min((long)p.frames * (p.region_rows + p.tile_tokens), (long)p.frames * p.T);
+    p.layer_cap = std::min((long)p.frames * p.region_rows, (long)p.frames * p.T);
     p.map_stride = p.cross ? (long)p.frames * p.T : (long)p.T;
     p.seg_space = p.cross ? (long)p.frames * p.num_tiles : p.num_tiles;
     const long map_entries = (long)p.frames * p.map_stride;
+    long span = p.T;
+    if (p.cross) span = (long)(p.window > 0 ? std::min(p.window, p.frames) : p.frames) * p.T;
+    // descriptors serve the bf16 kernel only
+    p.gd_stride = p.dtype == 1 ? 4 * ((span + 63) / 64) : 0;
+    const long gd_entries = (long)p.frames * p.gd_stride;
     p.frame_segs.assign((size_t)p.frames, {});
     p.seg_n.assign((size_t)p.frames, std::vector<int>((size_t)p.seg_space, 0));
     p.seg_phys.assign((size_t)p.frames, std::vector<long>((size_t)p.seg_space, -1L));
@@ -383,24 +447,36 @@ int layer_setup(Pipeline& p) {
     p.seg_mark.assign((size_t)p.seg_space, 0);
     p.tile_phys.assign((size_t)p.frames * p.num_tiles, -1L);
     p.tile_gen.assign((size_t)p.frames * p.num_tiles, 0);
+    p.tile_rows.assign((size_t)p.frames * p.num_tiles, 0);
     p.tile_slots.assign((size_t)p.tile_tokens, -1L);
+    p.gd_dev.assign((size_t)p.frames, {});
     if (p.plan_only) {
         p.plan_map.assign((size_t)map_entries, -1L);
         p.plan_stamp.assign((size_t)map_entries, 0);
+        p.plan_gd.assign((size_t)gd_entries * 2, 0u);
         return 0;
     }
     p.layer_arena = static_cast<char*>(
         kvp_dev_alloc((size_t)std::max<long>(1, p.layer_cap * 2 * row_bytes)));
     p.layer_map = static_cast<long*>(kvp_dev_alloc((size_t)map_entries * sizeof(long)));
+    if (gd_entries > 0)
+        p.layer_gd = static_cast<unsigned*>(kvp_dev_alloc((size_t)gd_entries * 8));
     p.layer_stager = kvp_stager_create();
-    if (!p.layer_arena || !p.layer_map || !p.layer_stager) {
+    if (!p.layer_arena || !p.layer_map || (gd_entries > 0 && !p.layer_gd) || !p.layer_stager) {
+        layer_teardown(p);
         kvp::set_error("pipeline: layer arena / map allocation failed");
         return 1;
     }
-    // the device map starts as all -1, matching seg_n
+    // the device map starts as all -1 (matching seg_n), the descriptor
+    // tables as all "no arena row" (matching gd_dev)
     if (kvp_stage_run(p.layer_stager, nullptr, 0, nullptr, 0, p.layer_map, map_entries, nullptr,
-                      nullptr, 0, p.stream))
+                      nullptr, 0, p.stream) ||
+        kvp::fill_words(p.layer_gd, gd_entries * 2, 0u, p.stream)) {
+        const std::string err = kvp_last_error();
+        layer_teardown(p);
+        kvp::set_error("%s", err.c_str());
         return 1;
+    }
     return 0;
 }
 
@@ -408,8 +484,8 @@ int layer_setup(Pipeline& p) {
 // takes the decisions of plan_frame_host's row loop (batched per tile, same
 // order, same stop at a tile's first refused row), and the frame's mapped
 // rows are kept as segments in p.frame_segs[f] (and their tiles marked as
-// mapped this run). The host map is written for the last
-// frame of the layer only (introspection of the last step).
+// mapped this run, with the longest prefix mapped). The host map is written
+// for the last frame of the layer only (introspection of the last step).
 void plan_frame_layer(Pipeline& p, KVTileManager& mgr, int f, const char* k, const char* v) {
     const long T = p.T;
     const long row_bytes = (long)p.D * p.elem;
@@ -448,7 +524,11 @@ void plan_frame_layer(Pipeline& p, KVTileManager& mgr, int f, const char* k, con
         if (n > 0) {
             const long gsrc = src_f * p.num_tiles + tile;
             segs.push_back(Pipeline::Seg{p.cross ? gsrc : tile, gsrc, (int)n});
-            p.tile_gen[(size_t)gsrc] = p.layer_gen;
+            if (p.tile_gen[(size_t)gsrc] != p.layer_gen) {
+                p.tile_gen[(size_t)gsrc] = p.layer_gen;
+                p.tile_rows[(size_t)gsrc] = 0;
+            }
+            p.tile_rows[(size_t)gsrc] = std::max(p.tile_rows[(size_t)gsrc], (int)n);
         }
     }
 }
@@ -488,11 +568,11 @@ void layer_add_update(Pipeline& p, long index, long value, long n) {
             (int)std::min<long>(kvp::kLayerMapEntries, n - j)});
 }
 
-// Physical rows of the run: every tile some frame maps, a whole tile each,
-// in key order (tile id order is key-row order, across frames too), so the
-// arena rows of adjacent mapped tiles are adjacent and a 16-row copy group
-// of the attention kernel whose rows are all mapped is one run of arena
-// rows. One copy run table for all of them.
+// Physical rows of the run: every tile some frame maps, its longest mapped
+// prefix, in key order (tile id order is key-row order, across frames too),
+// so the arena rows of adjacent mapped tiles are adjacent and a 16-row copy
+// group of the attention kernel whose rows are all mapped is one run of
+// arena rows. One copy run table for all of them.
 int layer_assign(Pipeline& p) {
     const long T = p.T;
     const long ntiles = (long)p.frames * p.num_tiles;
@@ -500,9 +580,9 @@ int layer_assign(Pipeline& p) {
         if (p.tile_gen[(size_t)g] != p.layer_gen) continue;
         const long tile = g % p.num_tiles;
         const long row0 = (g / p.num_tiles) * T + tile * p.tile_tokens;
-        const long c = std::min((long)p.tile_tokens, T - tile * p.tile_tokens);
-        if (p.layer_nphys + c > 0x7fffffffL || row0 + c > 0x7fffffffL) {
-            kvp::set_error("pipeline: layer arena rows exceed int");
+        const long c = p.tile_rows[(size_t)g];
+        if (p.layer_nphys + c > p.layer_cap || row0 + c > 0x7fffffffL) {
+            kvp::set_error("pipeline: the layer maps more than its %ld arena rows", p.layer_cap);
             return 1;
         }
         p.tile_phys[(size_t)g] = p.layer_nphys;
@@ -551,26 +631,44 @@ void layer_collect(Pipeline& p, int f) {
     }
 }
 
-// Grow the layer arena to hold the run's physical rows (rare: a layer with
-// many partly mapped tiles). The old arena may still be read by earlier
-// launches on the stream, so the stream is drained first.
-int layer_reserve(Pipeline& p) {
-    if (p.layer_nphys <= p.layer_cap) return 0;
-    const long row_bytes = (long)p.D * p.elem;
-    const long cap = std::min(std::max(p.layer_nphys, 2 * p.layer_cap), (long)p.frames * p.T);
-    if (kvp_stream_sync(p.stream)) return 1;
-    kvp_dev_free(p.layer_arena);
-    p.layer_arena = static_cast<char*>(kvp_dev_alloc((size_t)cap * 2 * row_bytes));
-    if (!p.layer_arena) {
-        p.layer_cap = 0;
-        kvp::set_error("pipeline: layer arena growth to %ld rows failed", cap);
-        return 1;
+// Frame f's descriptor writes (bf16): the frame's segments encoded per
+// 16-row group of its key range, against the entries the device holds.
+void layer_gd_collect(Pipeline& p, int f) {
+    if (p.gd_stride == 0) return;
+    const long T = p.T;
+    const long rel = p.cross ? 0 : (long)f * T;
+    long b, e;
+    frame_range(p, f, b, e);
+    p.gd_subs.clear();
+    for (const Pipeline::Seg& s : p.frame_segs[(size_t)f]) {
+        const long row0 = (s.gsrc / p.num_tiles) * T + (s.gsrc % p.num_tiles) * p.tile_tokens;
+        kvp::gd::add_rows(p.gd_subs, row0 - rel, s.n, p.tile_phys[(size_t)s.gsrc], b, e);
     }
-    p.layer_cap = cap;
-    return 0;
+    kvp::gd::encode(p.gd_subs, p.gd_new);
+    // both lists are in group order: write what changed, clear what is gone
+    std::vector<kvp::gd::Ent>& old = p.gd_dev[(size_t)f];
+    const long base = (long)f * p.gd_stride;
+    size_t i = 0, j = 0;
+    while (i < old.size() || j < p.gd_new.size()) {
+        if (j == p.gd_new.size() || (i < old.size() && old[i].g < p.gd_new[j].g)) {
+            p.gd_writes.push_back(kvp::LayerGdWrite{base + old[i].g, 0u, 0u});
+            ++i;
+        } else if (i == old.size() || p.gd_new[j].g < old[i].g) {
+            p.gd_writes.push_back(kvp::LayerGdWrite{base + p.gd_new[j].g, p.gd_new[j].w0, p.gd_new[j].w1});
+            ++j;
+        } else {
+            if (old[i].w0 != p.gd_new[j].w0 || old[i].w1 != p.gd_new[j].w1)
+                p.gd_writes.push_back(
+                    kvp::LayerGdWrite{base + p.gd_new[j].g, p.gd_new[j].w0, p.gd_new[j].w1});
+            ++i;
+            ++j;
+        }
+    }
+    old.swap(p.gd_new);
 }
 
-// One attention launch over all frames of the layer.
+// One attention launch over all frames of the layer (the layer's arena,
+// map slices and, in bf16, descriptor tables).
 int layer_attention(Pipeline& p, const char* q, const char* k, const char* v, char* out) {
     kvp::AttnLaunch L;
     L.dtype = p.dtype;
@@ -582,6 +680,10 @@ int layer_attention(Pipeline& p, const char* q, const char* k, const char* v, ch
         L.arena = p.layer_arena;  // one arena for every frame
         L.kvmap = p.layer_map;
         L.map_fstride = p.map_stride;
+        if (!p.cold_rows_nt) {
+            L.gdesc = p.layer_gd;
+            L.gd_fstride = p.gd_stride;
+        }
     }
     L.nq = p.T;
     L.D = p.D;
@@ -604,12 +706,11 @@ int layer_attention(Pipeline& p, const char* q, const char* k, const char* v, ch
     return kvp::launch_attention(L);
 }
 
-// A whole layer: host plans of every frame, one staging launch for all
-// frames' arena regions and map slices, one attention launch.
 // The staging launch of a plan-only layer run, applied on the host: the
-// layer map and the physical rows' sources. Fails when two runs of the
-// launch would write one physical row or one map entry (the workgroups of
-// one launch run in no fixed order).
+// layer map, the descriptor tables and the physical rows' sources. Fails
+// when two runs of the launch would write one physical row, one map entry
+// or one descriptor entry (the workgroups of one launch run in no fixed
+// order).
 int layer_apply_host(Pipeline& p) {
     p.plan_src.assign((size_t)p.layer_nphys, -1L);
     for (const kvp::LayerCopyRun& r : p.layer_copies) {
@@ -634,12 +735,25 @@ int layer_apply_host(Pipeline& p) {
             p.plan_map[(size_t)e] = m.value < 0 ? -1L : (long)m.value + j;
         }
     }
+    std::vector<char> hit(p.plan_gd.size() / 2, 0);
+    for (const kvp::LayerGdWrite& w : p.gd_writes) {
+        if (w.index < 0 || 2 * w.index >= (long)p.plan_gd.size() || hit[(size_t)w.index]) {
+            kvp::set_error("pipeline: descriptor writes overlap or leave the table at %ld", w.index);
+            return 1;
+        }
+        hit[(size_t)w.index] = 1;
+        p.plan_gd[(size_t)(2 * w.index)] = w.w0;
+        p.plan_gd[(size_t)(2 * w.index + 1)] = w.w1;
+    }
     return 0;
 }
 
-// A whole layer: host plans of every frame, one staging launch (the copies
-// and map runs), one attention launch. Plan-only pipelines apply the staging
-// on the host instead and launch nothing.
+// A whole layer: host plans of every frame, one staging launch (the copies,
+// map runs and descriptor writes), one attention launch. Plan-only
+// pipelines apply the staging on the host instead and launch nothing. A
+// failure once the host mirrors of the device map and descriptor tables
+// have moved on tears the layer state down, so that the next run starts
+// from a fresh device map instead of one the mirrors no longer describe.
 int run_layer(Pipeline& p, const char* q, const char* k, const char* v, char* out,
               const float* scores_flat) {
     p.next_frame = 0;
@@ -656,20 +770,32 @@ int run_layer(Pipeline& p, const char* q, const char* k, const char* v, char* ou
     p.layer_nphys = 0;
     p.layer_copies.clear();
     p.layer_updates.clear();
+    p.gd_writes.clear();
     for (int f = 0; f < p.frames; ++f) {
         if (select_and_release(p, *p.layer_mgr, f, scores_flat)) return 1;
         plan_frame_layer(p, *p.layer_mgr, f, k, v);
         finish_frame(p, *p.layer_mgr, f);
     }
     if (layer_assign(p)) return 1;
-    for (int f = 0; f < p.frames; ++f) layer_collect(p, f);
-    if (p.plan_only) return layer_apply_host(p);
-    if (layer_reserve(p)) return 1;
-    if (kvp::layer_stage_launch(p.layer_stager, p.layer_arena, k, v, (long)p.D * p.elem,
-                                p.layer_copies.data(), (long)p.layer_copies.size(), p.layer_map,
-                                p.layer_updates.data(), (long)p.layer_updates.size(), p.stream))
-        return 1;
-    return layer_attention(p, q, k, v, out);
+    for (int f = 0; f < p.frames; ++f) {
+        layer_collect(p, f);
+        layer_gd_collect(p, f);
+    }
+    int rc = p.plan_only
+                 ? layer_apply_host(p)
+                 : kvp::layer_stage_launch(p.layer_stager, p.layer_arena, k, v,
+                                           (long)p.D * p.elem, p.layer_copies.data(),
+                                           (long)p.layer_copies.size(), p.layer_map,
+                                           p.layer_updates.data(), (long)p.layer_updates.size(),
+                                           p.layer_gd, p.gd_writes.data(),
+                                           (long)p.gd_writes.size(), p.stream);
+    if (rc == 0 && !p.plan_only) rc = layer_attention(p, q, k, v, out);
+    if (rc) {
+        const std::string err = kvp_last_error();
+        layer_teardown(p);
+        kvp::set_error("%s", err.c_str());
+    }
+    return rc;
 }
 
 }  // namespace
@@ -797,6 +923,35 @@ void* kvp_pipeline_layer_arena(void* p) { return PL(p)->layer_arena; }
 const long* kvp_pipeline_layer_map(void* p) { return PL(p)->layer_map; }
 long kvp_pipeline_layer_map_stride(void* p) { return PL(p)->map_stride; }
 long kvp_pipeline_layer_copied_rows(void* p) { return PL(p)->layer_nphys; }
+long kvp_pipeline_layer_arena_bytes(void* p) {
+    const Pipeline& pl = *PL(p);
+    return pl.layer_arena ? pl.layer_cap * 2L * pl.D * pl.elem : 0;
+}
+const unsigned* kvp_pipeline_layer_gd(void* p) { return PL(p)->layer_gd; }
+long kvp_pipeline_layer_gd_stride(void* p) { return PL(p)->gd_stride; }
+
+int kvp_pipeline_layer_attention(void* p, const void* q, const void* k, const void* v,
+                                 void* out) {
+    Pipeline& pl = *PL(p);
+    if (pl.plan_only || (pl.persist && !pl.layer_arena)) {
+        kvp::set_error("pipeline: no layer run to repeat");
+        return 1;
+    }
+    if (!check_data(pl, static_cast<const char*>(q), static_cast<const char*>(k),
+                    static_cast<const char*>(v), static_cast<const char*>(out)))
+        return 1;
+    return layer_attention(pl, static_cast<const char*>(q), static_cast<const char*>(k),
+                           static_cast<const char*>(v), static_cast<char*>(out));
+}
+
+long kvp_pipeline_layer_plan_gd(void* p, int f, unsigned* out, long cap) {
+    const Pipeline& pl = *PL(p);
+    if (!pl.plan_only || f < 0 || f >= pl.frames || pl.plan_gd.empty()) return -1;
+    const long n = std::min(pl.gd_stride, cap);
+    if (n > 0)
+        memcpy(out, pl.plan_gd.data() + (size_t)f * 2 * pl.gd_stride, (size_t)n * 2 * sizeof(unsigned));
+    return pl.gd_stride;
+}
 
 long kvp_pipeline_layer_plan_map(void* p, int f, long* out, long cap) {
     const Pipeline& pl = *PL(p);

@@ -91,6 +91,10 @@ SIGNATURES = {
     "kvp_attn_forward_frames": (c_int, [c_int, c_void_p, c_void_p, c_void_p, c_void_p, c_long,
                                         c_void_p, c_long, c_void_p, c_int, c_int, c_int, c_int,
                                         c_int, c_int, c_int, c_void_p]),
+    "kvp_attn_forward_frames_gd": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_long,
+                                           c_void_p, c_long, c_void_p, c_long, c_void_p, c_int,
+                                           c_int, c_int, c_int, c_int, c_int, c_void_p]),
+    "kvp_attn_group_desc": (c_long, [c_long_p, c_long, c_long, c_int, c_void_p, c_long]),
     "kvp_set_stream": (None, [c_void_p]),
     "kvp_get_stream": (c_void_p, []),
     "kvp_last_error": (c_char_p, []),
@@ -134,6 +138,12 @@ SIGNATURES = {
     "kvp_pipeline_layer_copied_rows": (c_long, [c_void_p]),
     "kvp_pipeline_layer_plan_map": (c_long, [c_void_p, c_int, c_long_p, c_long]),
     "kvp_pipeline_layer_plan_sources": (c_long, [c_void_p, c_long_p, c_long]),
+    "kvp_pipeline_layer_plan_gd": (c_long, [c_void_p, c_int, c_void_p, c_long]),
+    "kvp_pipeline_layer_arena_bytes": (c_long, [c_void_p]),
+    "kvp_pipeline_layer_gd": (c_void_p, [c_void_p]),
+    "kvp_pipeline_layer_gd_stride": (c_long, [c_void_p]),
+    "kvp_pipeline_layer_attention": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p,
+                                             c_void_p]),
     # upstream K/V producer (reference: src/backbone.py:8-67), include/kvp_producer.h
     "kvp_layer_norm": (c_int, [c_int, c_int, c_void_p, c_void_p, c_void_p, c_void_p, c_long,
                                c_int, ctypes.c_float, c_void_p]),

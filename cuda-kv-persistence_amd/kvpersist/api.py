@@ -295,6 +295,40 @@ def attn_forward_frames(dtype: int, q, k, v, arena, kvmap, out, frames: int, T: 
            "attn_forward_frames")
 
 
+def attn_forward_frames_gd(q, k, v, arena, kvmap, gdesc, out, frames: int, T: int, D: int,
+                           heads: int, *, cross: bool, gd_frame_stride: int,
+                           window_frames: int = 0, arena_frame_bytes: int = 0,
+                           map_frame_stride: int = 0, stream: int | None = None) -> None:
+    """attn_forward_frames for bf16 with the map's group descriptors (frame
+    f's table at gdesc + 8 * f * gd_frame_stride bytes); see
+    kvp_attn_forward_frames_gd in kvp_c_api.h."""
+    _check(_lib.load().kvp_attn_forward_frames_gd(_ptr(q), _ptr(k), _ptr(v), _ptr(arena),
+                                                  arena_frame_bytes, _ptr(kvmap),
+                                                  map_frame_stride, _ptr(gdesc), gd_frame_stride,
+                                                  _ptr(out), frames, T, D, heads, int(cross),
+                                                  window_frames, stream),
+           "attn_forward_frames_gd")
+
+
+def attn_group_desc(kvmap, key_begin: int, key_end: int, D: int) -> np.ndarray:
+    """Group-descriptor table of one frame's KVMap slice (host int64 array
+    indexed by key row) over the key range [key_begin, key_end): uint32
+    array [entries, 2]; see kvp_attn_group_desc in kvp_c_api.h."""
+    m = np.ascontiguousarray(kvmap, dtype=np.int64)
+    if key_end > len(m):
+        raise ValueError("attn_group_desc: key range past the map")
+    lib = _lib.load()
+    mp = m.ctypes.data_as(_lib.c_long_p)
+    n = int(lib.kvp_attn_group_desc(mp, key_begin, key_end, D, None, 0))
+    if n < 0:
+        raise RuntimeError(f"attn_group_desc: {_lib.last_error()}")
+    out = np.zeros((n, 2), dtype=np.uint32)
+    if n:
+        _check(0 if lib.kvp_attn_group_desc(mp, key_begin, key_end, D, out.ctypes.data, n) == n
+               else 1, "attn_group_desc")
+    return out
+
+
 def attn_splits(dtype: int, nq: int, heads: int, frames: int, span: int) -> int:
     return int(_lib.load().kvp_attn_splits(dtype, nq, heads, frames, span))
 
@@ -425,3 +459,29 @@ class FramePipeline:
 
     def layer_map_stride(self) -> int:
         return int(self._lib.kvp_pipeline_layer_map_stride(self._h))
+
+    def layer_arena_bytes(self) -> int:
+        return int(self._lib.kvp_pipeline_layer_arena_bytes(self._h))
+
+    # group descriptors of the layer map (bf16 layer runs)
+    def layer_gd_ptr(self) -> int:
+        return int(self._lib.kvp_pipeline_layer_gd(self._h) or 0)
+
+    def layer_gd_stride(self) -> int:
+        return int(self._lib.kvp_pipeline_layer_gd_stride(self._h))
+
+    def layer_plan_gd(self, f: int) -> np.ndarray:
+        """Plan-only, after run(): frame f's descriptor table, uint32 [stride, 2]."""
+        n = int(self._lib.kvp_pipeline_layer_plan_gd(self._h, f, None, 0))
+        if n < 0:
+            raise RuntimeError("layer_plan_gd: not a plan-only pipeline after run()")
+        buf = np.zeros((n, 2), dtype=np.uint32)
+        if n:
+            self._lib.kvp_pipeline_layer_plan_gd(self._h, f, buf.ctypes.data, n)
+        return buf
+
+    def layer_attention(self, q, k, v, out) -> None:
+        """The last run()'s attention launch again, alone (same arena, map
+        slices and descriptors) on the pipeline's stream."""
+        _check(self._lib.kvp_pipeline_layer_attention(self._h, _ptr(q), _ptr(k), _ptr(v),
+                                                      _ptr(out)), "pipeline layer_attention")

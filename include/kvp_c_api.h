@@ -167,8 +167,10 @@ int kvp_attn_forward_range_noalloc(int dtype, const void* q, const void* k,
  * frames run as one grid, longest key range first, with no key split.
  * flags: KVP_ATTN_COLD_ROWS_NT = with a KVMap (bf16), rows read from the
  * original K/V buffers are loaded non-temporally, so the L2 evicts them
- * before arena lines (the CDNA4 counterpart of the reference's persisting
- * window with streaming misses, src/kv_tile_manager.cu:39-47). */
+ * before arena lines. An additive CDNA4 residency lever with no
+ * counterpart in the reference: its persisting window (hitRatio 1,
+ * src/kv_tile_manager.cu:39-47) streams no access, and rows outside the
+ * window are cached normally there. */
 #define KVP_ATTN_COLD_ROWS_NT 1
 int kvp_attn_forward_frames(int dtype, const void* q, const void* k,
                             const void* v, const void* arena,
@@ -176,6 +178,39 @@ int kvp_attn_forward_frames(int dtype, const void* q, const void* k,
                             long map_frame_stride, void* out, int frames,
                             int T, int D, int heads, int cross,
                             int window_frames, int flags, void* stream);
+
+/* kvp_attn_forward_frames for bf16 KVMap launches with group descriptors
+ * (additive; no counterpart in the reference). gdesc: per frame,
+ * gd_frame_stride entries of two 32-bit words, frame f's table at
+ * gdesc + 2*f*gd_frame_stride. Entry g describes rows [b + 16g, b + 16g + 16)
+ * of frame f's key range [b, e) (rows at or past e excluded), the copy
+ * group of one wave of the bf16 kernel; gd_frame_stride must cover
+ * 4 * ceil(longest range / 64) entries. Entry (w0, w1):
+ *   w0 == 0     no row of the group is read from the arena;
+ *   w0 == 1     general: the kernel reads the group's KVMap entries;
+ *   w0 bit 31   sub-run: rows r0 .. r0+n-1 of the group map to arena rows
+ *               l .. l+n-1 (l = bits 0-22, r0 = bits 23-26, n-1 = bits
+ *               27-30); w1 is a second sub-run word or 0; every other row
+ *               of the group maps to no arena row.
+ * The table must describe the map exactly (kvp_attn_group_desc builds it
+ * from a host copy of a map slice). With it the kernel reads a group's map
+ * entries only for general groups; outputs are bitwise those of
+ * kvp_attn_forward_frames with the same map. */
+int kvp_attn_forward_frames_gd(const void* q, const void* k, const void* v,
+                               const void* arena, long arena_frame_bytes,
+                               const long* kvmap, long map_frame_stride,
+                               const unsigned* gdesc, long gd_frame_stride,
+                               void* out, int frames, int T, int D, int heads,
+                               int cross, int window_frames, void* stream);
+/* Host builder of one frame's descriptor table: map[j] is the KVMap entry
+ * of key j (the slice the frame reads), [key_begin, key_end) the frame's key
+ * range, D the hidden size (an entry m counts as an arena row when
+ * 0 <= m and 2*(m+1)*2*D <= 2^32, as in the bf16 kernel). Writes the
+ * 4*ceil((key_end-key_begin)/64) entries (2 words each) to out when cap
+ * (in entries) holds them; returns the entry count, or -1 on bad
+ * arguments. */
+long kvp_attn_group_desc(const long* map, long key_begin, long key_end, int D,
+                         unsigned* out, long cap);
 
 void kvp_set_stream(void* stream);
 void* kvp_get_stream(void);
@@ -246,19 +281,25 @@ int kvp_pipeline_step(void* p, int f, const void* q, const void* k,
                       const void* v, void* out, const float* scores_flat);
 /* A whole layer, frames 0..frames-1 (streaming state is reset first), in
  * two launches: every frame's host plan is made first, then one staging
- * launch copies every row any frame maps into a layer arena, once per row
- * (physical rows in first-mapped order; K and V are fixed for the layer, so
- * the copy serves every frame that maps the row), and writes frame f's
- * KVMap to slice f of a layer map, pointing each row frame f maps at its
- * physical row; then one attention launch runs all frames, frame f reading
- * its own slice. Each frame maps exactly the rows frame-by-frame stepping
- * maps, so outputs equal stepping bit for bit. The layer arena holds
- * min(frames x rows-per-set-aside, frames*T) rows of [K | V]; the layer map
- * holds frames slices of frames*T (cross) or T (intra) entries, absolute key
- * rows in cross mode, frame-relative in intra mode. A plan-only pipeline
- * makes the same plans and applies the staging launch's runs to host copies
- * of the map and of each physical row's source row, launching nothing
- * (kvp_pipeline_layer_plan_map / _plan_sources). */
+ * launch copies the rows the frames map into a layer arena and writes frame
+ * f's KVMap to slice f of a layer map, pointing each row frame f maps at its
+ * physical row (and, in bf16, the group descriptors of every slice, see
+ * kvp_attn_forward_frames_gd); then one attention launch runs all frames,
+ * frame f reading its own slice. K and V are fixed for the layer, so one
+ * copy of a row serves every frame that maps it: each tile some frame maps
+ * gets physical rows for the longest prefix of it any frame maps, tiles in
+ * key order. The layer arena is allocated once at frames x rows-per-set-
+ * aside rows of [K | V] (the set-aside summed over the frames; no frame maps
+ * more than the set-aside, so the run always fits). Each frame maps exactly
+ * the rows frame-by-frame stepping maps: outputs are bitwise equal across
+ * policies and modes within kvp_pipeline_run, and equal stepping's up to
+ * the rounding of stepping's key split. The layer map holds frames slices
+ * of frames*T (cross) or T (intra) entries, absolute key rows in cross mode,
+ * frame-relative in intra mode. A plan-only pipeline makes the same plans
+ * and applies the staging launch's runs to host copies of the map, the
+ * descriptor tables and each physical row's source row, launching nothing
+ * (kvp_pipeline_layer_plan_map / _plan_gd / _plan_sources). After a failed
+ * run the layer state is rebuilt from scratch by the next run. */
 int kvp_pipeline_run(void* p, const void* q, const void* k, const void* v,
                      void* out, const float* scores_flat);
 /* Introspection of the last step. */
@@ -279,12 +320,26 @@ void* kvp_pipeline_layer_arena(void* p);
 const long* kvp_pipeline_layer_map(void* p);
 long kvp_pipeline_layer_map_stride(void* p);
 long kvp_pipeline_layer_copied_rows(void* p);
+/* Bytes allocated for the layer arena (0 before the first run). */
+long kvp_pipeline_layer_arena_bytes(void* p);
+/* Group descriptors of the layer map (bf16; NULL otherwise): frame f's
+ * table at gd + 2*f*stride words. */
+const unsigned* kvp_pipeline_layer_gd(void* p);
+long kvp_pipeline_layer_gd_stride(void* p);
+/* The attention launch of the last kvp_pipeline_run again (same arena, map
+ * slices and descriptors), on the pipeline's stream: the kernel the run
+ * timed alone. Returns 0 on success. */
+int kvp_pipeline_layer_attention(void* p, const void* q, const void* k,
+                                 const void* v, void* out);
 /* Plan-only pipelines, after kvp_pipeline_run: slice f of the layer map
  * (returns map_stride, copies min(map_stride, cap) entries) and the K/V row
  * each physical row holds (returns the row count, copies min(count, cap));
  * -1 for pipelines that are not plan-only or before the first run. */
 long kvp_pipeline_layer_plan_map(void* p, int f, long* out, long cap);
 long kvp_pipeline_layer_plan_sources(void* p, long* out, long cap);
+/* Plan-only: frame f's descriptor table (returns the stride in entries,
+ * copies min(stride, cap) entries of 2 words); -1 as above. */
+long kvp_pipeline_layer_plan_gd(void* p, int f, unsigned* out, long cap);
 
 #ifdef __cplusplus
 }

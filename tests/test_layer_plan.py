@@ -12,17 +12,22 @@ entry twice. For every frame f of the layer:
   * each mapped row points at a physical row whose source is that row, rows
     of one frame at distinct physical rows;
 a row keeps one physical row across the layer, physical rows are handed out
-a whole tile at a time in key order (the copied rows are the rows of every
-tile some frame maps, ascending), and the last frame's introspection (selected ids, staged tiles,
-rows copied, slot map, streaming bytes) equals the oracle's. Layers are run
-back to back with different scores, so the map runs also cover entries that
-change or go back to -1 between runs.
+a tile at a time in key order, each tile the longest prefix of it any frame
+maps (the copied rows are those prefixes, ascending; never more than
+frames x rows-per-set-aside), and the last frame's introspection (selected
+ids, staged tiles, rows copied, slot map, streaming bytes) equals the
+oracle's. In bf16, each frame's group-descriptor table equals the table
+kvp_attn_group_desc builds from that frame's map slice (two separate
+encoders: the pipeline's from its tile segments, the builder's from the
+entries). Layers are run back to back with different scores, so the map
+runs and descriptor writes also cover entries that change or go back to -1
+/ 0 between runs.
 """
 
 import numpy as np
 import pytest
 
-from kvpersist import FramePipeline, workloads
+from kvpersist import FramePipeline, api, workloads
 from oracle import manager as mm
 
 D = workloads.HIDDEN
@@ -55,7 +60,8 @@ def _check_layer(pl, policy, *, cross, streaming, frames, T, set_aside, elem, sc
     assert src.size == pl.layer_copied_rows()
     stride = frames * T if cross else T
     phys_of = {}
-    touched = set()
+    prefix = {}  # tile -> longest mapped prefix over the frames
+    tiles = (T + TILE - 1) // TILE
     for f in range(frames):
         sl = pl.layer_plan_map(f)
         assert sl.size == stride
@@ -74,12 +80,29 @@ def _check_layer(pl, policy, *, cross, streaming, frames, T, set_aside, elem, sc
         np.testing.assert_array_equal(src[phys], rows + rows0, err_msg=f"sources, frame {f}")
         for r, ph in zip((rows + rows0).tolist(), phys.tolist()):
             assert phys_of.setdefault(r, ph) == ph, (f, r)
-            touched.add(r // T * ((T + TILE - 1) // TILE) + (r % T) // TILE)
-    # whole tiles: each touched tile's rows, once, in key order (so the rows
-    # of adjacent mapped tiles sit in adjacent arena rows)
-    rows_of = {g: min(TILE, T - (g % ((T + TILE - 1) // TILE)) * TILE) for g in touched}
-    assert src.size == sum(rows_of.values())
-    assert (np.diff(src) > 0).all()
+        # each tile's mapped rows are a prefix of it
+        per_tile = {}
+        for r in (rows + rows0).tolist():
+            g = r // T * tiles + (r % T) // TILE
+            per_tile.setdefault(g, []).append(r - (r // T * T + (r % T) // TILE * TILE))
+        for g, offs in per_tile.items():
+            assert sorted(offs) == list(range(len(offs))), (f, g)
+            prefix[g] = max(prefix.get(g, 0), len(offs))
+        if elem == 2:
+            b = max(0, f + 1 - window) * T if (cross and window) else 0
+            e = (f + 1) * T if cross else T
+            want_gd = api.attn_group_desc(sl, b, e, D)
+            got_gd = pl.layer_plan_gd(f)
+            n = want_gd.shape[0]
+            assert got_gd.shape[0] >= n
+            np.testing.assert_array_equal(got_gd[:n], want_gd, err_msg=f"descriptors, frame {f}")
+            assert (got_gd[n:] == 0).all(), f
+    # each touched tile's longest mapped prefix, once, in key order (so the
+    # rows of adjacent fully mapped tiles sit in adjacent arena rows)
+    want_src = [g // tiles * T + (g % tiles) * TILE + j for g in sorted(prefix)
+                for j in range(prefix[g])]
+    np.testing.assert_array_equal(src, want_src)
+    assert src.size <= frames * (set_aside // (2 * D * elem))
 
 
 CASES = [
