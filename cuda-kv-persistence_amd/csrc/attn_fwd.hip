@@ -283,18 +283,22 @@ __device__ __forceinline__ float softmax_update(float (&s)[N], float scale_log2,
 // Softmax: scores stay in the log2 domain (scale folded into one FMA before
 // v_exp_f32). Exponentials are taken against the running max without
 // computing the tile max; the running max is raised (and O, l rescaled
-// together, wave-uniform branch) only when a row sum would exceed 2^64 or is
-// not finite — on the first tile and on strong score growth. O/l is
-// unchanged mathematically; p stays within bf16/fp32 range.
+// together, wave-uniform branch) only when a tile's row sum would exceed the
+// tile's key count (64) or is not finite — on the first tile and when scores
+// rise above the running max. O/l is unchanged mathematically. Bounding
+// each tile's sum by its key count bounds O by (keys so far) x max|V| and l
+// by the key count, as the reference's update with every p <= 1 does
+// (src/gated_attention_kernel.cu:101-115): fp32 O stays finite for every V
+// the reference's stays finite for.
 // ---------------------------------------------------------------------------
 
 constexpr int kBf16TileBytes = kBf16BlockKeys * kHeadDim * 2;  // 16 KiB
 // Raw buffer descriptor word 3 for gfx9-family (32-bit data format, no
 // swizzle): out-of-range offsets (>= num_records) read as zero.
 constexpr int kBufFlags = 0x00020000;
-// Row-sum bound of one tile's exponentials (2^64): below it every p fits
-// bf16/fp32 comfortably and O, l accumulate without rescaling.
-constexpr float kRowSumLimit = 18446744073709551616.0f;
+// Row-sum bound of one bf16 tile's exponentials: its key count (see the
+// softmax note above).
+constexpr float kRowSumLimit = (float)kBf16BlockKeys;
 constexpr unsigned kVSwzTable = 0xAC60u;  // nibbles {0, 6, 12, 10}
 // Buffer offset past the records of every bf16 tile descriptor (a tile
 // covers at most 64 rows of 2*D bytes): a load there reads no memory and
@@ -1244,10 +1248,12 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_bf16_kernel(AttnArgs a) 
 // 64-bit address per lane; the entries of tile t+2 are loaded into
 // registers during tile t.
 // Softmax as in the bf16 kernel: exponentials against the running max, the
-// max raised (and O, l rescaled) only when a tile's row sum exceeds 2^64 or
-// is not finite; P stays fp32.
+// max raised (and O, l rescaled) only when a tile's row sum exceeds the
+// tile's key count (32) or is not finite; P stays fp32.
 // ---------------------------------------------------------------------------
 
+// Row-sum bound of one fp32 tile's exponentials: its key count.
+constexpr float kF32RowSumLimit = (float)kF32BlockKeys;
 constexpr int kF32TileBytes = kF32BlockKeys * kHeadDim * 4;  // 16 KiB
 
 template <bool kMap>
@@ -1434,7 +1440,7 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_f32_kernel(AttnArgs a) {
             return rs + other_half(rs);
         };
         float tot = exp_tile(m_run);
-        if (__builtin_amdgcn_ballot_w64(!(tot <= kRowSumLimit))) {
+        if (__builtin_amdgcn_ballot_w64(!(tot <= kF32RowSumLimit))) {
             float mx = s[0];
 #pragma unroll
             for (int v = 1; v < 16; ++v) mx = fmaxf(mx, s[v]);

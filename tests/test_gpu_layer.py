@@ -347,3 +347,36 @@ def test_split_launches_on_two_streams_match_serial_runs():
     for i in range(2):
         for rep in range(4):
             assert torch.equal(outs[i][rep], serial[i]), (i, rep)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_softmax_keeps_o_finite_where_the_reference_does(dtype):
+    """Unsplit layer launch (two frames, so no key split) on inputs where the
+    scores jump by ~57 (log2 units) after the first tile and stay there, with
+    V positive and ~2^64. The reference's online softmax keeps every weight
+    <= 1 (src/gated_attention_kernel.cu:101-115), so its accumulator stays
+    near keys x 2^64 ~ 2^73; an update that let a tile's weights sum to 2^63
+    before rescaling would accumulate ~2^130 and overflow fp32. The output
+    (the mean of the plateau keys' V rows) must be finite and match the
+    float64 softmax within the precision bar, scaled by 2^64."""
+    frames, T, heads = 2, 576, 1
+    D = heads * 128
+    scale = 2.0 ** 64
+    q = torch.zeros(frames * T, D)
+    q[:, 0] = 32.0
+    k = torch.zeros(frames * T, D)
+    for f in range(frames):
+        k[f * T + 64:(f + 1) * T, 0] = 14.0  # q.k = 448: 57.1 in log2 units
+    rng = np.random.default_rng(3)
+    v = torch.from_numpy(rng.uniform(0.5, 1.5, (frames * T, D)).astype(np.float32)) * scale
+    if dtype == torch.bfloat16:
+        q, k, v = at.round_bf16(q), at.round_bf16(k), at.round_bf16(v)
+    qd, kd, vd = (x.to(DEV).to(dtype).contiguous() for x in (q, k, v))
+    got = _layer(dtype, qd, kd, vd, frames, T, heads, "intra").double().cpu()
+    assert torch.isfinite(got).all()
+    for f in range(frames):
+        sl = slice(f * T, (f + 1) * T)
+        s = (q[sl].double() @ k[sl].double().T) / np.sqrt(128.0)
+        want = torch.softmax(s, dim=-1) @ v[sl].double()
+        err = float((got[sl] - want).abs().max()) / scale
+        assert err <= (FP32_MAX if dtype == torch.float32 else BF16_MAX), err
