@@ -41,6 +41,7 @@
 #include <cstdint>
 #include <cstdio>
 #include <mutex>
+#include <thread>
 #include <vector>
 
 #include "kvp_c_api.h"
@@ -466,9 +467,11 @@ __device__ __forceinline__ void store_rows_staged(const AttnArgs& a, const WgCoo
 // no per-row source selection in its copy path.
 // kColdNt (KVMap launches only): rows read from the original K/V buffers
 // (not from the arena) are loaded non-temporally (the nt cache-policy bit),
-// so the L2 evicts them first and keeps the arena's lines: the counterpart of
-// the reference's access-policy window, whose misses stream
-// (src/kv_tile_manager.cu:39-47, missProp = cudaAccessPropertyStreaming).
+// so the L2 evicts them first and keeps the arena's lines. An additive
+// residency lever of this build: the reference's access-policy window
+// (src/kv_tile_manager.cu:39-47) has hitRatio 1, so none of its accesses
+// take the streaming miss property, and rows outside the window are cached
+// normally there.
 // kCyclic: the launch's ranges are cut by a window, and workgroups walk
 // upward from their round's start key with a wrap (decode_wg); otherwise
 // they walk upward from the range start, or downward when reversed.
@@ -1618,14 +1621,23 @@ std::mutex g_mu;
 std::vector<DeviceInfo> g_dev_info;
 // Split-partial workspace, one buffer per (device, stream): launches on one
 // stream reuse its buffer in stream order, launches on different streams
-// never share one. Buffers live until the process ends.
+// never share one. hipStreamPerThread is one handle value for every thread
+// but a different stream in each, so its buffers are also keyed by thread.
+// At most kMaxWorkspaces buffers per device are kept: a launch on another
+// stream frees the least recently used one first (hipFree waits for the
+// device, so no launch still reads it); kvp_attn_workspace_release frees a
+// stream's buffer at once.
+constexpr int kMaxWorkspaces = 8;
 struct Workspace {
     int dev = -1;
     void* stream = nullptr;
+    std::thread::id tid;  // hipStreamPerThread only
     void* ptr = nullptr;
     size_t bytes = 0;
+    unsigned long use = 0;  // last use, for the eviction order
 };
 std::vector<Workspace> g_ws;
+unsigned long g_ws_clock = 0;
 
 int current_device() {
     int d = 0;
@@ -1654,16 +1666,34 @@ DeviceInfo device_info(int dev) {
     return di;
 }
 
+std::thread::id stream_thread(void* stream) {
+    return stream == static_cast<void*>(hipStreamPerThread) ? std::this_thread::get_id()
+                                                            : std::thread::id();
+}
+
+// Caller holds g_mu.
+void free_workspace_at(size_t i) {
+    if (g_ws[i].ptr) (void)hipFree(g_ws[i].ptr);
+    g_ws.erase(g_ws.begin() + (long)i);
+}
+
 void* workspace(int dev, void* stream, size_t bytes) {
     std::lock_guard<std::mutex> lk(g_mu);
-    Workspace* wp = nullptr;
-    for (Workspace& w : g_ws)
-        if (w.dev == dev && w.stream == stream) wp = &w;
-    if (!wp) {
-        g_ws.push_back(Workspace{dev, stream, nullptr, 0});
-        wp = &g_ws.back();
+    const std::thread::id tid = stream_thread(stream);
+    long found = -1, n_dev = 0, lru = -1;
+    for (size_t i = 0; i < g_ws.size(); ++i) {
+        if (g_ws[i].dev != dev) continue;
+        ++n_dev;
+        if (g_ws[i].stream == stream && g_ws[i].tid == tid) found = (long)i;
+        if (lru < 0 || g_ws[i].use < g_ws[(size_t)lru].use) lru = (long)i;
     }
-    Workspace& w = *wp;
+    if (found < 0) {
+        if (n_dev >= kMaxWorkspaces) free_workspace_at((size_t)lru);
+        g_ws.push_back(Workspace{dev, stream, tid, nullptr, 0, 0});
+        found = (long)g_ws.size() - 1;
+    }
+    Workspace& w = g_ws[(size_t)found];
+    w.use = ++g_ws_clock;
     if (w.bytes < bytes) {
         // Growing waits for the in-flight users of the old buffer: launches
         // on this same stream.
@@ -2068,6 +2098,26 @@ int attention_splits(int dtype, int nq, int heads, int frames, long span) {
 }
 
 }  // namespace kvp
+
+extern "C" int kvp_attn_workspace_release(void* stream) {
+    const int dev = kvp::current_device();
+    if (dev < 0) return 1;
+    (void)hipStreamSynchronize(static_cast<hipStream_t>(stream));
+    std::lock_guard<std::mutex> lk(kvp::g_mu);
+    const std::thread::id tid = kvp::stream_thread(stream);
+    for (size_t i = 0; i < kvp::g_ws.size(); ++i) {
+        if (kvp::g_ws[i].dev == dev && kvp::g_ws[i].stream == stream && kvp::g_ws[i].tid == tid) {
+            kvp::free_workspace_at(i);
+            break;
+        }
+    }
+    return 0;
+}
+
+extern "C" long kvp_attn_workspace_count(void) {
+    std::lock_guard<std::mutex> lk(kvp::g_mu);
+    return (long)kvp::g_ws.size();
+}
 
 extern "C" int kvp_attn_block_queries(int) { return kvp::kBlockQ; }
 extern "C" int kvp_attn_block_keys(int dtype) {

@@ -13,6 +13,10 @@
 void TileGatingPolicy::select_range(const float* scores_flat, long first_id,
                                     int num_candidates, int max_tiles,
                                     long* out_ids, int* out_count) {
+    if (ReuseWeightedPolicy* rw = dynamic_cast<ReuseWeightedPolicy*>(this)) {
+        rw->select_window(scores_flat, first_id, num_candidates, max_tiles, out_ids, out_count);
+        return;
+    }
     select(scores_flat ? scores_flat + first_id : nullptr, num_candidates,
            max_tiles, out_ids, out_count);
     for (int i = 0; i < *out_count; ++i) out_ids[i] += first_id;
@@ -50,16 +54,16 @@ ReuseWeightedPolicy::ReuseWeightedPolicy(int tiles_per_frame, int total_frames)
 
 void ReuseWeightedPolicy::select(const float* scores_flat, int num_candidates,
                                  int max_tiles, long* out_ids, int* out_count) {
-    select_range(scores_flat, 0, num_candidates, max_tiles, out_ids, out_count);
+    select_window(scores_flat, 0, num_candidates, max_tiles, out_ids, out_count);
 }
 
 // reuse_weighted (reference: tile_gating_policy.cpp:32-68):
 //   rate_max = max(1e-6f, max score)            (float)
 //   prio(i)  = (total_frames - src_frame(i)) * (1 - min(1, s_i / rate_max))
 // computed in double; sort by prio descending, then id ascending.
-void ReuseWeightedPolicy::select_range(const float* scores_flat, long first_id,
-                                       int num_candidates, int max_tiles,
-                                       long* out_ids, int* out_count) {
+void ReuseWeightedPolicy::select_window(const float* scores_flat, long first_id,
+                                        int num_candidates, int max_tiles,
+                                        long* out_ids, int* out_count) {
     const int n = std::max(0, num_candidates);
     const float* s = scores_flat + first_id;
     float rate_max = 1e-6f;

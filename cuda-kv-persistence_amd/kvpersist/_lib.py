@@ -95,6 +95,8 @@ SIGNATURES = {
                                            c_void_p, c_long, c_void_p, c_long, c_void_p, c_int,
                                            c_int, c_int, c_int, c_int, c_int, c_void_p]),
     "kvp_attn_group_desc": (c_long, [c_long_p, c_long, c_long, c_int, c_void_p, c_long]),
+    "kvp_attn_workspace_release": (c_int, [c_void_p]),
+    "kvp_attn_workspace_count": (c_long, []),
     "kvp_set_stream": (None, [c_void_p]),
     "kvp_get_stream": (c_void_p, []),
     "kvp_last_error": (c_char_p, []),

@@ -212,6 +212,15 @@ int kvp_attn_forward_frames_gd(const void* q, const void* k, const void* v,
 long kvp_attn_group_desc(const long* map, long key_begin, long key_end, int D,
                          unsigned* out, long cap);
 
+/* Split-partial workspaces (per-frame launches that split their key range
+ * keep one device buffer per (device, stream), per thread for
+ * hipStreamPerThread; at most 8 per device, least recently used freed
+ * first). kvp_attn_workspace_release frees the calling device's buffer of
+ * `stream` after synchronising it (0 on success); kvp_attn_workspace_count
+ * is the number of buffers held on all devices. No reference counterpart. */
+int kvp_attn_workspace_release(void* stream);
+long kvp_attn_workspace_count(void);
+
 void kvp_set_stream(void* stream);
 void* kvp_get_stream(void);
 const char* kvp_last_error(void);

@@ -13,7 +13,9 @@
 // Additive: select_range() evaluates a policy over a sub-range of the
 // frame-major candidate list (used by sliding-window attention, where only
 // the last W frames are attendable). select_range(s, 0, n, ...) is
-// identical to select(s, n, ...).
+// identical to select(s, n, ...). It is a non-virtual member, so the class's
+// virtual table (destructor, select, name) is the reference's and a policy
+// compiled against the reference header is binary compatible.
 
 class TileGatingPolicy {
 public:
@@ -27,11 +29,12 @@ public:
     virtual const char* name() const = 0;
 
     // Candidates are scores_flat[first_id .. first_id + num_candidates);
-    // returned ids are absolute (first_id already added). The default
-    // forwards to select() on the shifted pointer.
-    virtual void select_range(const float* scores_flat, long first_id,
-                              int num_candidates, int max_tiles,
-                              long* out_ids, int* out_count);
+    // returned ids are absolute (first_id already added). Forwards to
+    // select() on the shifted pointer, except for ReuseWeightedPolicy, whose
+    // priorities depend on the absolute id (ReuseWeightedPolicy::select_window).
+    void select_range(const float* scores_flat, long first_id,
+                      int num_candidates, int max_tiles, long* out_ids,
+                      int* out_count);
 };
 
 // Control: persist nothing.
@@ -67,11 +70,11 @@ public:
     void select(const float* scores_flat, int num_candidates, int max_tiles,
                 long* out_ids, int* out_count) override;
     const char* name() const override;
-    // Window-aware: the source frame of candidate i is
-    // (first_id + i) / tiles_per_frame.
-    void select_range(const float* scores_flat, long first_id,
-                      int num_candidates, int max_tiles, long* out_ids,
-                      int* out_count) override;
+    // Window-aware form behind select_range: the source frame of candidate
+    // i is (first_id + i) / tiles_per_frame.
+    void select_window(const float* scores_flat, long first_id,
+                       int num_candidates, int max_tiles, long* out_ids,
+                       int* out_count);
 
 private:
     int tpf_;

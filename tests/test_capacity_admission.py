@@ -6,9 +6,9 @@ grounding config: 22 tiles of 98,304 B fill 2,162,688 B exactly, tile 23 is
 refused, duplicates never double-count, release frees room, clear resets,
 and the tile layout of 1560 tokens gives 98 tiles with a last count of 8.
 
-Admission is pure host bookkeeping, so this runs without a GPU: the admitted
-addresses are never dereferenced. On a GPU box they come from
-kvtm_dev_alloc, as in the reference.
+Admission is pure host bookkeeping, so the scenario runs without a GPU on
+host-only addresses (never dereferenced), and again, marked gpu, on tiles
+carved from kvtm_dev_alloc memory, as in the reference.
 """
 
 import ctypes
@@ -21,8 +21,8 @@ OK, REFUSED, INVALID = 1, 0, -1
 META = json.loads((Path(__file__).parent / "golden" / "reference_meta.json").read_text())
 
 
-def _scratch(lib, nbytes):
-    if lib.kvp_device_count() > 0:
+def _scratch(lib, nbytes, on_device):
+    if on_device:
         p = lib.kvtm_dev_alloc(nbytes)
         assert p, "scratch alloc failed"
         return p, True
@@ -30,6 +30,16 @@ def _scratch(lib, nbytes):
 
 
 def test_capacity_admission(lib):
+    _scenario(lib, on_device=False)
+
+
+@pytest.mark.gpu
+def test_capacity_admission_on_device_memory(lib):
+    assert lib.kvp_device_count() > 0
+    _scenario(lib, on_device=True)
+
+
+def _scenario(lib, on_device):
     g = META["grounding"]
     budget, tile_bytes = g["max_persisting_l2_bytes"], g["kv_tile_bytes"]
     expected = g["tiles_fully_persistable"]
@@ -39,7 +49,7 @@ def test_capacity_admission(lib):
 
     m = lib.kvtm_create(budget, max_window)
     assert m
-    scratch, on_device = _scratch(lib, budget + 4 * tile_bytes)
+    scratch, on_device = _scratch(lib, budget + 4 * tile_bytes, on_device)
     try:
         # S1: init + read-back of the configured limit
         assert lib.kvtm_init(m) == 1

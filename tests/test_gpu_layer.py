@@ -380,3 +380,36 @@ def test_softmax_keeps_o_finite_where_the_reference_does(dtype):
         want = torch.softmax(s, dim=-1) @ v[sl].double()
         err = float((got[sl] - want).abs().max()) / scale
         assert err <= (FP32_MAX if dtype == torch.float32 else BF16_MAX), err
+
+
+def test_split_workspaces_stay_bounded_across_streams():
+    """Split launches on ten streams in turn: each stream's result equals the
+    first, the library keeps at most 8 split workspaces on the device (least
+    recently used freed), and releasing every stream's buffer leaves none of
+    them behind."""
+    from kvpersist import _lib
+    lib = _lib.load()
+    nq, keys, heads = 700, 4000, 4
+    D = heads * 128
+    g = torch.Generator(device=DEV).manual_seed(11)
+    q, k, v = (torch.randn(n, D, generator=g, device=DEV).to(torch.bfloat16)
+               for n in (nq, keys, keys))
+    assert api.attn_splits(api.BF16, nq, heads, 1, keys) > 1
+    torch.cuda.synchronize()
+    streams = [torch.cuda.Stream() for _ in range(10)]
+    outs = []
+    for st in streams:
+        o = torch.empty_like(q)
+        assert lib.kvp_attn_forward_range(api.BF16, q.data_ptr(), k.data_ptr(), v.data_ptr(),
+                                          None, None, o.data_ptr(), nq, D, heads, 0, keys,
+                                          st.cuda_stream) == 0
+        st.synchronize()
+        outs.append(o)
+        assert lib.kvp_attn_workspace_count() <= 8
+    for o in outs[1:]:
+        assert torch.equal(o, outs[0])
+    before = lib.kvp_attn_workspace_count()
+    for st in streams:
+        assert lib.kvp_attn_workspace_release(st.cuda_stream) == 0
+    # the last 8 streams held buffers (the first two were evicted)
+    assert lib.kvp_attn_workspace_count() == before - 8

@@ -255,3 +255,56 @@ def test_run_layer_arena_and_maps_match_oracle_plan(dtype, streaming):
     assert torch.equal(outs["motion"], outs["none"])
     tol = 2e-5 if dtype == torch.float32 else 1.6e-2
     assert float((outs["motion"].float() - stepped.float()).abs().max()) <= tol
+
+
+def test_failed_layer_run_leaves_the_next_run_correct():
+    """A layer run whose staging launch is refused (K and V 2 bytes off
+    16-byte alignment: refused on the host, nothing reaches the device)
+    fails after the pipeline's host mirrors of the device map and descriptor
+    tables were updated for it. The next run must still leave every map
+    slice and descriptor table exactly as a plan-only pipeline plans them
+    for that run's scores, and give policy none's output bit for bit."""
+    from kvpersist import _lib, api
+    lib = _lib.load()
+    cfg = workloads.CONFIGS["c3"]
+    frames, T = 3, cfg.tokens
+    _, _, _, qd, kd, vd = _device_inputs(frames, T, torch.bfloat16, seed=17)
+    rng = np.random.default_rng(17)
+    tiles = (T + 15) // 16
+    sa, sb, sc = (rng.random((frames, tiles), dtype=np.float32) for _ in range(3))
+    kw = dict(cross=True, streaming=False, frames=frames, T=T, D=D, heads=HEADS,
+              tile_tokens=16, set_aside_bytes=cfg.set_aside, dtype=api.BF16)
+    pl = FramePipeline("motion", **kw)
+    out = torch.empty_like(qd)
+    pl.set_scores(sa)
+    pl.run(qd, kd, vd, out)
+    torch.cuda.synchronize()
+    # the same K/V bytes, 2 bytes off alignment
+    kbuf = torch.empty(kd.numel() + 8, dtype=torch.bfloat16, device=DEV)
+    vbuf = torch.empty_like(kbuf)
+    kbuf[1:1 + kd.numel()] = kd.view(-1)
+    vbuf[1:1 + vd.numel()] = vd.view(-1)
+    pl.set_scores(sb)
+    with pytest.raises(RuntimeError):
+        pl.run(qd, kbuf[1:1 + kd.numel()].view_as(kd), vbuf[1:1 + vd.numel()].view_as(vd), out)
+    pl.set_scores(sc)
+    pl.run(qd, kd, vd, out)
+    torch.cuda.synchronize()
+    plan = FramePipeline("motion", plan_only=True, **kw)
+    plan.set_scores(sc)
+    plan.run()
+    stride, gstride = pl.layer_map_stride(), pl.layer_gd_stride()
+    for f in range(frames):
+        np.testing.assert_array_equal(_layer_map(pl, f, stride), plan.layer_plan_map(f),
+                                      err_msg=f"slice {f}")
+        gd = np.empty((gstride, 2), dtype=np.uint32)
+        assert lib.kvp_memcpy_d2h(gd.ctypes.data, pl.layer_gd_ptr() + 8 * f * gstride,
+                                  gd.nbytes, None) == 0
+        np.testing.assert_array_equal(gd, plan.layer_plan_gd(f), err_msg=f"descriptors {f}")
+    nb = FramePipeline("none", **kw)
+    ref = torch.empty_like(qd)
+    nb.run(qd, kd, vd, ref)
+    torch.cuda.synchronize()
+    assert torch.equal(out, ref)
+    for p in (pl, plan, nb):
+        p.close()

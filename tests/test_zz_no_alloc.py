@@ -5,7 +5,15 @@ Both run the same kernels on the same launch plan; only where the split
 partials live differs (the library's fixed device scratch array instead of
 an allocated workspace), so the outputs must be equal bit for bit. Each case
 makes two calls in a row, the second with a smaller input, so the second
-call runs over scratch contents the first one left.
+call runs over scratch contents the first one left. The allocation-free call
+goes first, on a stream no launch has used, and the library's count of
+split workspaces must not change across it (had it fallen back to the
+allocating path, that stream would now hold one); the allocating call after
+it creates that stream's workspace, which kvp_attn_workspace_release frees.
+The entry's refusal of partials above its 64 MiB array cannot be reached on
+this GPU: a one-frame launch splits only while its workgroups underfill the
+CUs x 2 slots, which bounds the fp32 partials at 512 x 128 x 128 x 4 B
+(33.5 MB).
 """
 
 import numpy as np
@@ -45,16 +53,28 @@ def _both(dtype, nq, keys, heads, key_begin, seed, with_map=False):
         kvmap = m.to(DEV)
     ref = torch.empty_like(q)
     got = torch.empty_like(q)
-    stream = torch.cuda.current_stream().cuda_stream
+    torch.cuda.synchronize()
+    side = torch.cuda.Stream()  # never used by a launch of this library
+    stream = side.cuda_stream
     args = (dt, q.data_ptr(), k.data_ptr(), v.data_ptr(),
             arena.data_ptr() if arena is not None else None,
             kvmap.data_ptr() if kvmap is not None else None)
-    assert lib.kvp_attn_forward_range(*args, ref.data_ptr(), nq, D, heads, key_begin, keys,
-                                      stream) == 0, lib.kvp_last_error()
+    n0 = lib.kvp_attn_workspace_count()
     assert lib.kvp_attn_forward_range_noalloc(*args, got.data_ptr(), nq, D, heads, key_begin,
                                               keys, stream) == 0, lib.kvp_last_error()
-    torch.cuda.synchronize()
-    return got, ref, api.attn_splits(dt, nq, heads, 1, keys - key_begin)
+    side.synchronize()
+    assert lib.kvp_attn_workspace_count() == n0, "the allocation-free entry made a workspace"
+    assert lib.kvp_attn_forward_range(*args, ref.data_ptr(), nq, D, heads, key_begin, keys,
+                                      stream) == 0, lib.kvp_last_error()
+    side.synchronize()
+    splits = api.attn_splits(dt, nq, heads, 1, keys - key_begin)
+    if splits > 1:
+        # one more buffer, unless the per-device bound of 8 evicted another
+        assert lib.kvp_attn_workspace_count() == min(n0 + 1, max(n0, 8))
+    n1 = lib.kvp_attn_workspace_count()
+    assert lib.kvp_attn_workspace_release(stream) == 0
+    assert lib.kvp_attn_workspace_count() == n1 - (1 if splits > 1 else 0)
+    return got, ref, splits
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
