@@ -1,19 +1,33 @@
-"""Run-to-run spread and policy separation of fabric read bytes (C4 workload).
+"""Run-to-run spread and policy separation of fabric read bytes.
 
 Restates the reference's variance study (reference: tests/test_variance.py:1-240)
-on MI355X with rocprofv3 counters instead of Nsight Compute:
+on MI355X with rocprofv3 counters instead of Nsight Compute, on two shapes
+(`--shape`):
 
-* workload: C4 — 50 query frames of 1560 tokens, causal
+* `c4`: 50 query frames of 1560 tokens, causal
   cross-frame attention over a sliding window of 8 frames, 12 heads x 128,
-  bf16, one layer (the reference's `policy_experiment` also runs one
-  attention launch per frame), synthetic device N(0,1) Q/K/V and the C4
-  camera-pan motion field; arena budget 22 bf16 tiles;
-* combos: {dense (arena), stream (sticky slots)} x {none, uniform, recency,
-  motion, reuse_weighted} (the reference's `COMBOS`, :153-155, plus uniform,
-  the fifth policy of its policy file);
+  bf16, arena budget 22 bf16 tiles; combos {dense (arena), stream (sticky
+  slots)} x {none, uniform, recency, motion, reuse_weighted} (the
+  reference's `COMBOS`, :153-155, plus uniform, the fifth policy of its
+  policy file);
+* `dense50` (the shape of the reference's published scoreboard,
+  docs/results/freeze_scoreboard.md:9-35, tests/test_policy_variants.py:
+  209-222): 50 query frames of 1560 tokens, fp32, full causal prefix (frame
+  f attends every key of frames 0..f), 12 heads x 128, set-aside 2,162,688 B
+  = 11 fp32 tiles (the reference driver's slot count for its RTX 3060
+  carve-out, src/run_policy_experiment.cu:143-144); combos {dense, stream} x
+  {none, recency, motion, reuse_weighted}, the reference's own four;
+* both: one layer, one attention launch per frame (kvp_pipeline_step, as the
+  reference's `policy_experiment`), synthetic device N(0,1) Q/K/V (seed 42)
+  and, unless `--motion-csv` gives a trace, the synthetic C4 motion field
+  (50 x 98 tiles, camera-pan drift; `workloads.motion_for`) — the
+  reference's scoreboard used its real-video trace, which needs OpenCV and a
+  download;
 * each frame is one attention launch (kvp_pipeline_step: frame by frame on
   one arena, the reference driver's sequence), so the launch window below
-  counts frames as the reference's does;
+  counts frames as the reference's does; a frame whose launch splits its key
+  range also runs a combine launch, counted with it (the reference's kernel
+  has no split);
 * each run profiles the attention launches of the run; the window is
   launches SKIP..SKIP+COUNT-1 = 34..49 (reference :39);
 * metric: L2->fabric read bytes per window (`FETCH_SIZE`, KiB, scaled by the
@@ -35,7 +49,7 @@ cannot pin MI355X clocks, and fabric bytes do not depend on the clock.
 
 Usage on the GPU box, from the repository root:
 
-    python3 -m kvpersist.variance [--smoke] [--out profiles/variance_c4.md]
+    python3 -m kvpersist.variance [--shape c4|dense50] [--smoke] [--out FILE]
                                   [--motion-csv motion_trace_real.csv]
 
 The analysis functions (`window_bytes`, `abba_orders`, `combo_stats`,
@@ -64,6 +78,18 @@ POLICIES = ("none", "uniform", "recency", "motion", "reuse_weighted")
 COMBOS = [(m, p) for m in MODES for p in POLICIES]
 KERNEL = "attn_fwd_bf16_kernel"
 
+# dtype, window (frames, 0 = full prefix), set-aside bytes, policies, the
+# attention kernel and the split-combine kernel counted with it
+SHAPES = {
+    "c4": dict(dtype="bf16", window=8, set_aside=None, policies=POLICIES,
+               kernel=KERNEL, follow="attn_combine_kernel",
+               title="C4 (50 frames, window 8, bf16)"),
+    "dense50": dict(dtype="fp32", window=0, set_aside=2162688,
+                    policies=("none", "recency", "motion", "reuse_weighted"),
+                    kernel="attn_fwd_f32_kernel", follow="attn_combine_kernel",
+                    title="dense50 (50 frames, full causal prefix, fp32, 11-tile set-aside)"),
+}
+
 ROOT = Path(__file__).resolve().parents[2]
 
 
@@ -74,21 +100,32 @@ def abba_orders(combos, repeats):
     return [list(combos) if r % 2 == 0 else list(reversed(combos)) for r in range(repeats)]
 
 
-def window_bytes(rows, skip=SKIP, count=COUNT, kernel=KERNEL, counter="FETCH_SIZE"):
+def window_bytes(rows, skip=SKIP, count=COUNT, kernel=KERNEL, counter="FETCH_SIZE",
+                 follow=None):
     """Per-launch counter values of the kernel's launches skip..skip+count-1.
 
     rows: dicts with Dispatch_Id, Kernel_Name, Counter_Name, Counter_Value
     (rocprofv3 counter_collection.csv). Launches are ordered by dispatch id.
+    Dispatches of a `follow` kernel (the split combine) count toward the
+    kernel launch dispatched before them.
     """
-    per = {}
+    per, extra = {}, {}
     for r in rows:
-        if kernel not in r["Kernel_Name"] or r["Counter_Name"] != counter:
+        if r["Counter_Name"] != counter:
             continue
+        name = r["Kernel_Name"]
         d = int(r["Dispatch_Id"])
-        per[d] = per.get(d, 0.0) + float(r["Counter_Value"])
+        if kernel in name:
+            per[d] = per.get(d, 0.0) + float(r["Counter_Value"])
+        elif follow and follow in name:
+            extra[d] = extra.get(d, 0.0) + float(r["Counter_Value"])
     ids = sorted(per)
     if len(ids) < skip + count:
         raise ValueError(f"{counter}: {len(ids)} {kernel} launches, window needs {skip + count}")
+    for d, val in extra.items():
+        owner = [i for i in ids if i < d]
+        if owner:
+            per[owner[-1]] += val
     return [per[d] for d in ids[skip:skip + count]]
 
 
@@ -137,20 +174,24 @@ def separated(stats, mode, a="reuse_weighted", b="recency"):
 
 # ------------------------------------------------------------------ child --
 
-def child(mode, policy, out_json):
-    """One C4 run (one layer, 50 frames); writes the output digest."""
+def child(shape, mode, policy, out_json):
+    """One run of the shape (one layer, 50 frames); writes the output digest."""
     sys.path.insert(0, str(ROOT / "cuda-kv-persistence_amd"))
     import torch
-    from kvpersist import BF16, FramePipeline, workloads
+    from kvpersist import BF16, FP32, FramePipeline, workloads
 
+    sh = SHAPES[shape]
     cfg = workloads.CONFIGS["c4"]
     T, D, H, F = cfg.tokens, workloads.HIDDEN, workloads.HEADS, cfg.frames
-    q, k, v = workloads.qkv_device(F, T, seed=42, dtype=torch.bfloat16, device="cuda")
+    fp32 = sh["dtype"] == "fp32"
+    q, k, v = workloads.qkv_device(F, T, seed=42,
+                                   dtype=torch.float32 if fp32 else torch.bfloat16,
+                                   device="cuda")
     out = torch.empty_like(q)
     pl = FramePipeline(policy, cross=True, streaming=(mode == "stream"), frames=F, T=T, D=D,
                        heads=H, tile_tokens=workloads.TILE_TOKENS,
-                       set_aside_bytes=cfg.set_aside,
-                       dtype=BF16, window_frames=cfg.window)
+                       set_aside_bytes=sh["set_aside"] or cfg.set_aside,
+                       dtype=FP32 if fp32 else BF16, window_frames=sh["window"])
     trace = os.environ.get(TRACE_ENV)
     if trace:
         from kvpersist.motion import read_trace_csv
@@ -163,19 +204,23 @@ def child(mode, policy, out_json):
     for f in range(F):
         pl.step(f, q, k, v, out)
     torch.cuda.synchronize()
-    digest = hashlib.sha256(out.view(torch.int16).cpu().numpy().tobytes()).hexdigest()
+    digest = hashlib.sha256(out.view(torch.int16 if not fp32 else torch.int32)
+                            .cpu().numpy().tobytes()).hexdigest()
     pl.close()
     Path(out_json).write_text(json.dumps({"mode": mode, "policy": policy, "sha256": digest}))
 
 
 # ----------------------------------------------------------------- parent --
 
-def _profiled(counters, mode, policy, workdir, tag, timeout):
+def _profiled(counters, shape, mode, policy, workdir, tag, timeout):
     d = Path(workdir) / tag
     digest = Path(workdir) / f"{tag}.json"
-    cmd = ["rocprofv3", "--pmc", *counters, "--kernel-include-regex", KERNEL,
+    sh = SHAPES[shape]
+    cmd = ["rocprofv3", "--pmc", *counters, "--kernel-include-regex",
+           f"{sh['kernel']}|{sh['follow']}",
            "--output-format", "csv", "-d", str(d), "-o", "p", "--",
-           sys.executable, "-m", "kvpersist.variance", "--child", mode, policy, str(digest)]
+           sys.executable, "-m", "kvpersist.variance", "--shape", shape,
+           "--child", mode, policy, str(digest)]
     env = dict(os.environ, TMPDIR=os.environ.get("TMPDIR", "/tmp"))
     env["PYTHONPATH"] = str(ROOT / "cuda-kv-persistence_amd") + os.pathsep + env.get("PYTHONPATH", "")
     # own process group: a run that overstays its limit is killed with the
@@ -207,10 +252,14 @@ def _fetch_factor():
 
 def main(argv=None):
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--shape", default="c4", choices=sorted(SHAPES))
     ap.add_argument("--child", nargs=3, metavar=("MODE", "POLICY", "OUT"))
     ap.add_argument("--smoke", action="store_true", help="one combo, one repeat")
-    ap.add_argument("--out", default=str(ROOT / "profiles" / "variance_c4.md"))
+    ap.add_argument("--out", default=None,
+                    help="report path (default profiles/variance_<shape>.md)")
     ap.add_argument("--timeout", type=int, default=180, help="seconds per profiled run")
+    ap.add_argument("--hit-repeats", type=int, default=REPEATS,
+                    help="repeats that also run the L2 hit-rate pass")
     ap.add_argument("--motion-csv", default=None,
                     help="motion trace CSV (frame_id,tile_id,motion_score,...; 50 x 98 rows) "
                          "instead of the synthetic C4 scores, as the reference runs its "
@@ -219,13 +268,16 @@ def main(argv=None):
     if args.motion_csv:
         os.environ[TRACE_ENV] = str(Path(args.motion_csv).resolve())
     if args.child:
-        child(*args.child)
+        child(args.shape, *args.child)
         return 0
     if not shutil.which("rocprofv3"):
         print("rocprofv3 not found", file=sys.stderr)
         return 2
+    sh = SHAPES[args.shape]
+    out_path = args.out or str(ROOT / "profiles" / f"variance_{args.shape}.md")
     factor = _fetch_factor()
-    combos = COMBOS[:1] if args.smoke else COMBOS
+    shape_combos = [(m, p) for m in MODES for p in sh["policies"]]
+    combos = shape_combos[:1] if args.smoke else shape_combos
     repeats = 1 if args.smoke else REPEATS
     results = {c: [] for c in combos}
     digests = {}
@@ -233,27 +285,36 @@ def main(argv=None):
         for r, order in enumerate(abba_orders(combos, repeats)):
             for mode, policy in order:
                 tag = f"{mode}_{policy}_r{r}"
-                rows, dg = _profiled(["FETCH_SIZE"], mode, policy, work, tag + "_fetch",
-                                     args.timeout)
-                fetch = [x * 1024.0 * factor for x in window_bytes(rows)]
-                hrows, _ = _profiled(["TCC_HIT_sum", "TCC_MISS_sum"], mode, policy, work,
-                                     tag + "_hit", args.timeout)
-                hit = window_bytes(hrows, counter="TCC_HIT_sum")
-                miss = window_bytes(hrows, counter="TCC_MISS_sum")
-                rate = sum(hit) / max(1.0, sum(hit) + sum(miss))
+                rows, dg = _profiled(["FETCH_SIZE"], args.shape, mode, policy, work,
+                                     tag + "_fetch", args.timeout)
+                fetch = [x * 1024.0 * factor
+                         for x in window_bytes(rows, kernel=sh["kernel"], follow=sh["follow"])]
+                rate = None
+                if r < args.hit_repeats:
+                    hrows, _ = _profiled(["TCC_HIT_sum", "TCC_MISS_sum"], args.shape, mode,
+                                         policy, work, tag + "_hit", args.timeout)
+                    hit = window_bytes(hrows, kernel=sh["kernel"], follow=sh["follow"],
+                                       counter="TCC_HIT_sum")
+                    miss = window_bytes(hrows, kernel=sh["kernel"], follow=sh["follow"],
+                                        counter="TCC_MISS_sum")
+                    rate = sum(hit) / max(1.0, sum(hit) + sum(miss))
                 digests[(mode, policy, r)] = dg
                 results[(mode, policy)].append({"launches": fetch, "sum": sum(fetch),
                                                 "hit_rate": rate})
-                print(f"[r{r}] {mode}/{policy}: window fabric reads {sum(fetch) / 1e9:.3f} GB, "
-                      f"L2 hit {100 * rate:.2f} %", flush=True)
+                print(f"[r{r}] {mode}/{policy}: window fabric reads {sum(fetch) / 1e9:.3f} GB"
+                      + (f", L2 hit {100 * rate:.2f} %" if rate is not None else ""),
+                      flush=True)
     gate = all(digests[(m, p, r)] == digests[(m, "none", r)]
                for (m, p, r) in digests if (m, "none", r) in digests)
     stats = {c: combo_stats([x["sum"] for x in results[c]], [x["launches"] for x in results[c]])
              for c in combos}
-    md = ["# Fabric-read variance and policy separation — C4 (50 frames, window 8, bf16)\n",
-          "Command (MI355X, repo root): `python3 -m kvpersist.variance` — per run two "
-          "`rocprofv3 --pmc` passes (`FETCH_SIZE`; `TCC_HIT_sum TCC_MISS_sum`) restricted to "
-          f"`{KERNEL}`; window = attention launches {SKIP}..{SKIP + COUNT - 1} of 50; "
+    md = [f"# Fabric-read variance and policy separation — {sh['title']}\n",
+          f"Command (MI355X, repo root): `python3 -m kvpersist.variance --shape {args.shape}"
+          + (f" --hit-repeats {args.hit_repeats}" if args.hit_repeats != REPEATS else "")
+          + "` — per run a `rocprofv3 --pmc FETCH_SIZE` pass (and, in the first "
+          f"{min(args.hit_repeats, repeats)} repeat(s), a `TCC_HIT_sum TCC_MISS_sum` pass) "
+          f"restricted to `{sh['kernel']}` and `{sh['follow']}` (a frame's split combine "
+          f"counted with its launch); window = frames {SKIP}..{SKIP + COUNT - 1} of 50; "
           f"{repeats} repeat(s), ABBA order; reads scaled x{factor:g} (copy calibration).\n",
           "Motion scores: " + (f"`{Path(args.motion_csv).name}` (`--motion-csv`)"
                                if args.motion_csv else
@@ -265,11 +326,11 @@ def main(argv=None):
     all_pass = True
     for c in combos:
         s = stats[c]
-        hits = sorted(x["hit_rate"] for x in results[c])
+        hits = sorted(x["hit_rate"] for x in results[c] if x["hit_rate"] is not None)
         all_pass &= s["pass"]
         md.append(f"| {c[0]} | {c[1]} | {s['median'] / 1e9:.4f} GB | {s['min'] / 1e9:.4f} | "
                   f"{s['max'] / 1e9:.4f} | {100 * s['spread']:.2f} % | "
-                  f"{100 * hits[len(hits) // 2]:.2f} % | "
+                  + (f"{100 * hits[len(hits) // 2]:.2f} %" if hits else "n/a") + " | "
                   f"{'PASS' if s['pass'] else 'FAIL (excursion)'} |")
         if s["hot_launches"]:
             md.append(f"  - launches with > 20 % range: {len(s['hot_launches'])}/{COUNT} "
@@ -294,7 +355,7 @@ def main(argv=None):
     text = "\n".join(md) + "\n"
     print(text)
     if not args.smoke:
-        Path(args.out).write_text(text)
+        Path(out_path).write_text(text)
     return 0 if gate else 1
 
 

@@ -35,6 +35,23 @@ def test_window_sums_per_dispatch_and_ignores_other_counters():
     assert va.window_bytes(doubled) == [2 * (100.0 + i) for i in range(34, 50)]
 
 
+def test_window_counts_a_frames_combine_with_its_launch():
+    # every third launch is followed by a combine dispatch (value 1e9)
+    got = va.window_bytes(_rows(50), follow="attn_combine_kernel")
+    assert got == [100.0 + i + (1e9 if i % 3 == 0 else 0.0) for i in range(34, 50)]
+    f32 = [dict(r, Kernel_Name=r["Kernel_Name"].replace("bf16", "f32")) for r in _rows(50)]
+    assert va.window_bytes(f32, kernel="attn_fwd_f32_kernel", follow="attn_combine_kernel") == got
+
+
+def test_shapes_follow_the_reference_scoreboard():
+    d = va.SHAPES["dense50"]
+    assert d["dtype"] == "fp32" and d["window"] == 0 and d["set_aside"] == 2162688
+    # 11 fp32 tiles of 16 rows x (K + V) x 1536 x 4 B (reference driver slot count)
+    assert d["set_aside"] // (16 * 1536 * 4 * 2) == 11
+    assert d["policies"] == ("none", "recency", "motion", "reuse_weighted")
+    assert va.SHAPES["c4"]["window"] == 8
+
+
 def test_window_needs_enough_launches():
     with pytest.raises(ValueError):
         va.window_bytes(_rows(49))
