@@ -69,6 +69,9 @@ def parse():
                     help="frame-units of the CPU baseline sample (frames 0..1 of one layer = 3)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--streaming", action="store_true", help="sticky-slot arena mode")
+    ap.add_argument("--step-mode", action="store_true",
+                    help="profile child: frames one at a time (kvp_pipeline_step, the "
+                         "reference driver's sequence) instead of the layer launch")
     ap.add_argument("--profile-policy", default=None,
                     help="run exactly one 30-layer step of this policy's pipeline and exit "
                          "(for rocprofv3 --pmc byte counting per policy)")
@@ -459,35 +462,42 @@ def motion_cpu_baseline(frames):
 
 POLICIES = ("none", "uniform", "recency", "motion", "reuse_weighted")
 ATTN_KERNEL = "attn_fwd_bf16_kernel"
-STAGE_KERNELS = ("stage_kernel", "stage_runs_kernel", "map_fill_kernel", "attn_combine")
+# a split launch's combine belongs to its attention launch (frame-by-frame
+# mode only; the layer launch never splits)
+COMBINE_KERNEL = "attn_combine_kernel"
+STAGE_KERNELS = ("stage_kernel", "stage_runs_kernel", "map_fill_kernel", "fill_words_kernel")
 COPY_KERNEL = "__amd_rocclr_copyBuffer"
 CALIB_BYTES = 256 << 20
 CALIB_COPIES = 4
 
 
-def counter_run(counters, policy, args, workdir):
+def counter_run(counters, policy, args, workdir, config=None, step_mode=False, layers=None):
     """One rocprofv3 --pmc pass over `bench.py --profile-policy policy` (one
     step of that policy's pipeline plus the copy calibration) in a fresh
     child process; returns {counter: {kernel class: [per-dispatch value]}}
-    (FETCH_SIZE / WRITE_SIZE in KiB)."""
+    (FETCH_SIZE / WRITE_SIZE in KiB). step_mode: the child runs the frames
+    one at a time (kvp_pipeline_step) instead of the layer launch."""
     import csv
     import glob
     import subprocess
-    d = Path(workdir) / f"{'_'.join(counters)}_{policy}"
+    config = config or args.config
+    layers = layers or args.layers
+    d = Path(workdir) / (f"{'_'.join(counters)}_{config}_{policy}" + ("_step" if step_mode else ""))
     cmd = ["rocprofv3", "--pmc", *counters, "--output-format", "csv", "-d", str(d), "-o", "p",
            "--", sys.executable, str(ROOT / "bench.py"), "--profile-policy", policy,
-           "--config", args.config, "--layers", str(args.layers), "--steps", "1",
-           "--calibrate"]
-    if args.set_aside_tiles is not None:
+           "--config", config, "--layers", str(layers), "--steps", "1", "--calibrate"]
+    if args.set_aside_tiles is not None and config == args.config:
         cmd += ["--set-aside-tiles", str(args.set_aside_tiles)]
     if args.cold_rows_nt:
         cmd.append("--cold-rows-nt")
     if args.streaming:
         cmd.append("--streaming")
+    if step_mode:
+        cmd.append("--step-mode")
     env = dict(os.environ, TMPDIR=os.environ.get("TMPDIR", "/tmp"))
     proc = subprocess.Popen(cmd, cwd="/tmp", env=env, stdout=subprocess.DEVNULL,
                             stderr=subprocess.DEVNULL, start_new_session=True)
-    tag = f"rocprofv3 {' '.join(counters)} {policy}"
+    tag = f"rocprofv3 {' '.join(counters)} {config} {policy}" + (" step" if step_mode else "")
     try:
         rc = proc.wait(timeout=args.counter_timeout)
     except subprocess.TimeoutExpired:
@@ -512,7 +522,7 @@ def counter_run(counters, policy, args, workdir):
         out = {"attention": [], "staging": [], "copy": []}
         for key in sorted(per[c]):
             n = names[key]
-            if ATTN_KERNEL in n:
+            if ATTN_KERNEL in n or COMBINE_KERNEL in n:
                 out["attention"].append(per[c][key])
             elif any(k in n for k in STAGE_KERNELS):
                 out["staging"].append(per[c][key])
@@ -528,50 +538,86 @@ def counter_run(counters, policy, args, workdir):
     return res
 
 
+def counter_set(args, work, config, policies, frames_total, *, write_policy=None,
+                hit_policies=(), step_mode=False, layers=None):
+    """Fabric bytes per policy of one configuration from counter_run children:
+    FETCH_SIZE for every policy, WRITE_SIZE for write_policy, TCC hit rate
+    for hit_policies; each scaled by its own run's calibration copies.
+    Deltas are against policy none when it is among `policies`."""
+    res = {"policies": {}, "runs": []}
+    for pol in policies:
+        r = counter_run(["FETCH_SIZE"], pol, args, work, config, step_mode, layers)["FETCH_SIZE"]
+        factor = CALIB_BYTES / (sorted(r["copy"])[1] * 1024.0)
+        attn = sum(r["attention"]) * 1024.0 * factor
+        stage = sum(r["staging"]) * 1024.0 * factor
+        res["policies"][pol] = {
+            "attn_read_bytes_per_frame": round(attn / frames_total),
+            "all_kernels_read_bytes_per_frame": round((attn + stage) / frames_total),
+            "attn_launches": len(r["attention"]), "fetch_factor": round(factor, 4)}
+        res["runs"].append(f"FETCH_SIZE {config} {pol}" + (" step" if step_mode else ""))
+        log(f"counters {config}{' step' if step_mode else ''}: {pol} attention reads "
+            f"{attn / frames_total / 1e9:.4f} GB/frame (calibration x{factor:.3f})")
+    if write_policy:
+        w = counter_run(["WRITE_SIZE"], write_policy, args, work, config, step_mode,
+                        layers)["WRITE_SIZE"]
+        wfactor = CALIB_BYTES / (sorted(w["copy"])[1] * 1024.0)
+        res["policies"][write_policy]["attn_write_bytes_per_frame"] = round(
+            sum(w["attention"]) * 1024.0 * wfactor / frames_total)
+        res["policies"][write_policy]["write_factor"] = round(wfactor, 4)
+        res["runs"].append(f"WRITE_SIZE {config} {write_policy}")
+    for pol in hit_policies:
+        h = counter_run(["TCC_HIT_sum", "TCC_MISS_sum"], pol, args, work, config, step_mode,
+                        layers)
+        hit, miss = sum(h["TCC_HIT_sum"]["attention"]), sum(h["TCC_MISS_sum"]["attention"])
+        res["policies"][pol]["attn_l2_hit_rate"] = round(hit / max(1.0, hit + miss), 4)
+        res["runs"].append(f"TCC_HIT_sum TCC_MISS_sum {config} {pol}")
+    base = res["policies"].get("none")
+    if base:
+        for rec in res["policies"].values():
+            rec["attn_read_delta_vs_none"] = round(
+                rec["attn_read_bytes_per_frame"] / base["attn_read_bytes_per_frame"] - 1.0, 5)
+            rec["all_kernels_read_delta_vs_none"] = round(
+                rec["all_kernels_read_bytes_per_frame"]
+                / base["all_kernels_read_bytes_per_frame"] - 1.0, 5)
+    return res
+
+
 def measure_counters(args, cfg, headline):
-    """Fabric bytes per policy from rocprofv3 child runs (FETCH_SIZE for every
-    policy, WRITE_SIZE for the headline policy), each scaled by the reading of
-    the 256 MiB calibration copies of its own run."""
+    """Fabric bytes from rocprofv3 child runs, before this process touches the
+    GPU: the headline configuration (every policy; WRITE_SIZE for the
+    headline policy; L2 hit rate for none and it), its reference-exact
+    frame-by-frame leg (none and the headline policy), and, unless --no-legs,
+    C4 (every policy) and C5 (none and motion), L2 hit rate for none and
+    motion."""
     import shutil
     import tempfile
+    from kvpersist import workloads
     if not shutil.which("rocprofv3"):
         return {"error": "rocprofv3 not found"}
     t0 = time.perf_counter()
-    frames_total = args.layers * cfg.frames
-    res = {"counter_runs": [], "policies": {}}
+    out = {}
     with tempfile.TemporaryDirectory(prefix="kvp_bench_") as work:
-        for pol in POLICIES:
-            r = counter_run(["FETCH_SIZE"], pol, args, work)["FETCH_SIZE"]
-            factor = CALIB_BYTES / (sorted(r["copy"])[1] * 1024.0)
-            attn = sum(r["attention"]) * 1024.0 * factor
-            stage = sum(r["staging"]) * 1024.0 * factor
-            res["policies"][pol] = {
-                "attn_read_bytes_per_frame": round(attn / frames_total),
-                "all_kernels_read_bytes_per_frame": round((attn + stage) / frames_total),
-                "attn_launches": len(r["attention"]), "fetch_factor": round(factor, 4)}
-            res["counter_runs"].append(f"FETCH_SIZE {pol}")
-            log(f"counters: {pol} attention reads {attn / frames_total / 1e9:.4f} GB/frame "
-                f"(calibration x{factor:.3f})")
-        w = counter_run(["WRITE_SIZE"], headline, args, work)["WRITE_SIZE"]
-        wfactor = CALIB_BYTES / (sorted(w["copy"])[1] * 1024.0)
-        res["policies"][headline]["attn_write_bytes_per_frame"] = round(
-            sum(w["attention"]) * 1024.0 * wfactor / frames_total)
-        res["policies"][headline]["write_factor"] = round(wfactor, 4)
-        res["counter_runs"].append(f"WRITE_SIZE {headline}")
-        for pol in ("none", headline):
-            h = counter_run(["TCC_HIT_sum", "TCC_MISS_sum"], pol, args, work)
-            hit, miss = sum(h["TCC_HIT_sum"]["attention"]), sum(h["TCC_MISS_sum"]["attention"])
-            res["policies"][pol]["attn_l2_hit_rate"] = round(hit / max(1.0, hit + miss), 4)
-            res["counter_runs"].append(f"TCC_HIT_sum TCC_MISS_sum {pol}")
-    base = res["policies"]["none"]
-    for pol, rec in res["policies"].items():
-        rec["attn_read_delta_vs_none"] = round(
-            rec["attn_read_bytes_per_frame"] / base["attn_read_bytes_per_frame"] - 1.0, 5)
-        rec["all_kernels_read_delta_vs_none"] = round(
-            rec["all_kernels_read_bytes_per_frame"] / base["all_kernels_read_bytes_per_frame"]
-            - 1.0, 5)
-    res["seconds"] = round(time.perf_counter() - t0, 1)
-    return res
+        head = counter_set(args, work, args.config, POLICIES, args.layers * cfg.frames,
+                           write_policy=headline, hit_policies=("none", headline))
+        out["policies"] = head["policies"]
+        out["counter_runs"] = head["runs"]
+        step = counter_set(args, work, args.config, ("none", headline),
+                           args.layers * cfg.frames, step_mode=True)
+        out["step_mode"] = step["policies"]
+        out["counter_runs"] += step["runs"]
+        if not args.no_legs:
+            legs = {}
+            for name, pols in (("c4", POLICIES), ("c5", ("none", "motion"))):
+                if name == args.config:
+                    continue
+                c = workloads.CONFIGS[name]
+                r = counter_set(args, work, name, pols, args.layers * c.frames,
+                                hit_policies=("none", "motion"))
+                legs[name] = r["policies"]
+                out["counter_runs"] += r["runs"]
+            out["legs"] = legs
+    out["seconds"] = round(time.perf_counter() - t0, 1)
+    return out
 
 
 def fp32_legs(torch, stream, api, FramePipeline, workloads, reps=50):
@@ -703,18 +749,22 @@ def main():
         pl.set_cold_rows_nt(args.cold_rows_nt)
         return pl
 
-    def run_step(pl, data):
+    def run_step(pl, data, step_mode=False):
         for q, k, v, out, sc in data:
             pl.set_scores(sc)
-            pl.run(q, k, v, out)
+            if step_mode:
+                for f in range(pl.frames):
+                    pl.step(f, q, k, v, out)
+            else:
+                pl.run(q, k, v, out)
 
-    def timed(pl, data, steps):
+    def timed(pl, data, steps, step_mode=False):
         torch.cuda.synchronize()
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         t0 = time.perf_counter()
         e0.record()
         for _ in range(steps):
-            run_step(pl, data)
+            run_step(pl, data, step_mode)
         e1.record()
         torch.cuda.synchronize()
         wall = (time.perf_counter() - t0) * 1e3
@@ -745,13 +795,14 @@ def main():
         # one step (what the rocprofv3 passes count), then the calibration
         # copies; --steps > 1 also times steps 2.. (outside the profiler only)
         pl = make(cfg, args.profile_policy, set_aside)
-        run_step(pl, data)
+        run_step(pl, data, args.step_mode)
         torch.cuda.synchronize()
         rec = {"profile_policy": args.profile_policy, "config": args.config,
+               "step_mode": bool(args.step_mode),
                "set_aside_bytes": set_aside, "staged_tiles_last_frame": pl.staged_tiles(),
                "layers": layers, "frames": cfg.frames, "query_frames": layers * cfg.frames}
         if args.steps > 1:
-            ms, _ = timed(pl, data, args.steps - 1)
+            ms, _ = timed(pl, data, args.steps - 1, args.step_mode)
             rec["ms_per_frame"] = round(ms / cfg.frames, 4)
         pl.close()
         if args.calibrate:
@@ -790,6 +841,14 @@ def main():
                "attn_tflops": round(tf, 2), "attn_mfma_frac": round(tf / BF16_PEAK_TFLOPS, 4),
                "attn_kernel_reads_kvmap": pol != "none",
                "staged_tiles_last_frame": pl.staged_tiles()}
+        if pol != "none":
+            # the layer arena: allocated once at frames x set-aside (the
+            # reference's per-step arena summed over the frames), used by the
+            # rows the last layer's frames map (each tile's longest prefix)
+            rec["layer_arena_alloc_bytes"] = pl.layer_arena_bytes()
+            rec["layer_arena_used_bytes"] = pl.layer_copied_rows() * 2 * workloads.HIDDEN * 2
+            rec["layer_arena_bound_bytes"] = F * (set_aside // (2 * workloads.HIDDEN * 2)) \
+                * 2 * workloads.HIDDEN * 2
         c = (counters or {}).get("policies", {}).get(pol)
         if c:
             rec.update(c)
@@ -802,6 +861,30 @@ def main():
             pl.close()
         log(f"policy {pol}: {t / F:.4f} ms/frame, attention alone {lay_ms * layers / F:.4f} "
             f"ms/frame ({tf:.0f} TFLOP/s)")
+
+    # --- reference-exact leg: the same layers frame by frame (kvp_pipeline_step:
+    # the reference driver's sequence, one arena of set_aside bytes refilled per
+    # frame, the reference's slot layout and KVMap values, one attention launch
+    # per frame, key split + combine where a frame underfills the GPU) --------
+    step_leg = {}
+    step_ref = None
+    for pol in ("none", args.policy):
+        pl = make(cfg, pol, set_aside)
+        run_step(pl, data, True)
+        t, _ = timed(pl, data, max(1, min(2, args.steps)), True)
+        o0 = data[0][3].clone()
+        if step_ref is None:
+            step_ref = o0
+        step_leg[pol] = {"pipeline_ms_per_frame": round(t / F, 4),
+                         "bitwise_equal_to_none": bool(torch.equal(o0, step_ref)),
+                         "arena_bytes": set_aside if pol != "none" else 0}
+        c = (counters or {}).get("step_mode", {}).get(pol)
+        if c:
+            step_leg[pol].update(c)
+        pl.close()
+        log(f"step mode {pol}: {t / F:.4f} ms/frame")
+    step_leg["workload"] = (f"{args.config} frame by frame (kvp_pipeline_step): the reference "
+                            f"driver's per-frame sequence on one {set_aside:,}-byte arena")
 
     head = policies[args.policy]
     lay_ms = head["attn_kernel_ms_per_layer_launch"]
@@ -842,7 +925,16 @@ def main():
                 "attn_kernel_ms_per_frame": round(lm * layers / c.frames, 4),
                 "attn_tflops": round(tfl, 2), "attn_mfma_frac": round(tfl / BF16_PEAK_TFLOPS, 4),
                 "attn_launches_per_layer": 1, "key_splits": 1,
-                "bitwise_equal_to_none_layer0": bool(torch.equal(o_motion, out))}
+                "bitwise_equal_to_none_layer0": bool(torch.equal(o_motion, out)),
+                "layer_arena_alloc_bytes": pl.layer_arena_bytes(),
+                "layer_arena_used_bytes": pl.layer_copied_rows() * 2 * workloads.HIDDEN * 2}
+            leg_counters = (counters or {}).get("legs", {}).get(name)
+            if leg_counters:
+                comp = compulsory_read_bytes_per_frame(c)
+                for rec in leg_counters.values():
+                    rec["attn_read_vs_compulsory"] = round(
+                        rec["attn_read_bytes_per_frame"] / comp, 4)
+                legs[name]["fabric_reads_per_policy"] = leg_counters
             nb.close()
             pl.close()
             del data_leg
@@ -915,7 +1007,9 @@ def main():
         },
         "cpu_baseline": cpu,
         "policies": policies,
-        "counters": ({k: v for k, v in counters.items() if k != "policies"}
+        "reference_exact_step_mode": step_leg,
+        "counters": ({k: v for k, v in counters.items()
+                      if k not in ("policies", "step_mode", "legs")}
                      if counters else None),
         "legs": legs,
         "wall_ms_per_step": round(wall_step, 3),
