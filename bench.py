@@ -204,7 +204,7 @@ def producer_bench(args, torch, stream):
     every launch: LayerNorm (fp32 -> bf16, HBM-bound), the three q/k/v
     projections (one launch of the grouped proj_gemm kernel, MFMA-bound),
     intra-frame attention (all 8 frames in one launch) and out_proj with the
-    residual add (hipBLASLt)."""
+    residual add (the grouped projection kernel, one group, accumulating)."""
     from kvpersist import api
     from kvpersist import backbone as kb
 
@@ -306,7 +306,7 @@ def producer_bench(args, torch, stream):
                               f"attn_fwd_bf16_kernel intra-frame, {frames} frames, "
                               f"{att_flops} flop"),
             "out_proj": roof("mfma", out_flops, out_ms, BF16_PEAK_TFLOPS, "TFLOP/s",
-                             f"1 hipBLASLt GEMM + residual, {out_flops} flop"),
+                             f"proj_gemm_bf16_small_kernel, 1 group, fp32 residual added in the epilogue, {out_flops} flop"),
         },
     }
     if not args.no_cpu_baseline:

@@ -11,9 +11,11 @@
 //                       init). Normals come from SplitMix64 (Steele, Lea and
 //                       Flood, OOPSLA 2014) through the Box-Muller transform;
 //                       the values are this library's own, not torch's.
-//   linear()            y = x W^T + b (+ y), a plain hipBLASLt GEMM with a
-//                       bias epilogue (nn.Linear, backbone.py:13-14,44); one
-//                       cached plan per shape and dtype.
+//   linear()            y = x W^T + b (+ y) (nn.Linear, backbone.py:13-14,44):
+//                       the grouped bf16 projection kernel where it tiles the
+//                       shape, else the generic fp32-matrix-core kernel
+//                       (proj_gemm.hip); out_proj adds into the residual
+//                       stream in the epilogue.
 //   Backbone            token_embed -> blocks -> final_norm (backbone.py:58-67);
 //                       a block is LN -> q,k,v projections -> intra-frame
 //                       attention (this library's attention kernel, the
@@ -29,7 +31,6 @@
 // q/k/v and the attention output are bf16 (fp32 accumulation throughout).
 
 #include <hip/hip_runtime.h>
-#include <hipblaslt/hipblaslt.h>
 
 #include <cstdint>
 #include <cstring>
@@ -51,7 +52,6 @@ constexpr int kLnRowsPerBlock = 4;  // one wave per row
 constexpr float kLnEps = 1e-5f;     // nn.LayerNorm default
 constexpr int kHeadDim = 128;
 constexpr float kInitStd = 0.02f;   // reference: src/backbone.py:54
-constexpr size_t kGemmWorkspace = 32u << 20;
 
 // ---------------------------------------------------------------------------
 // device helpers
@@ -198,182 +198,22 @@ int launch_ok(const char* what) {
 }
 
 // ---------------------------------------------------------------------------
-// hipBLASLt linear layers
+// Linear layers: the grouped bf16 projection kernel for the shapes it tiles
+// (K % 64, N % 128, 16-byte aligned operands: every projection of the
+// reference's configuration), the generic fp32-matrix-core kernel for every
+// other shape and for fp32 (proj_gemm.hip). No library GEMM.
 // ---------------------------------------------------------------------------
-
-struct GemmKey {
-    int in_t, out_t;
-    long rows;
-    int K, N;
-    int acc, bias;
-    bool operator<(const GemmKey& o) const {
-        return std::tie(in_t, out_t, rows, K, N, acc, bias) <
-               std::tie(o.in_t, o.out_t, o.rows, o.K, o.N, o.acc, o.bias);
-    }
-};
-
-struct GemmPlan {
-    hipblasLtMatmulDesc_t desc = nullptr;
-    hipblasLtMatrixLayout_t la = nullptr, lb = nullptr, lc = nullptr;
-    hipblasLtMatmulAlgo_t algo;
-    size_t ws = 0;
-};
-
-struct StreamWorkspace {
-    void* ptr = nullptr;
-    size_t bytes = 0;
-};
-
-// Per device; kept until the process ends.
-struct GemmDevice {
-    hipblasLtHandle_t handle = nullptr;
-    std::map<GemmKey, GemmPlan> plans;
-    std::map<void*, StreamWorkspace> ws;  // one workspace per stream
-};
-
-std::mutex g_gemm_mu;
-std::vector<GemmDevice*> g_gemm;
-
-hipDataType hip_type(int dt) { return dt == 1 ? HIP_R_16BF : HIP_R_32F; }
-
-const char* status_text(hipblasStatus_t s) {
-    switch (s) {
-    case HIPBLAS_STATUS_SUCCESS: return "success";
-    case HIPBLAS_STATUS_NOT_INITIALIZED: return "not initialized";
-    case HIPBLAS_STATUS_ALLOC_FAILED: return "allocation failed";
-    case HIPBLAS_STATUS_INVALID_VALUE: return "invalid value";
-    case HIPBLAS_STATUS_ARCH_MISMATCH: return "arch mismatch";
-    case HIPBLAS_STATUS_EXECUTION_FAILED: return "execution failed";
-    case HIPBLAS_STATUS_NOT_SUPPORTED: return "not supported";
-    default: return "error";
-    }
-}
-
-#define KVP_LT(call, what)                                                              \
-    do {                                                                                \
-        const hipblasStatus_t s_ = (call);                                              \
-        if (s_ != HIPBLAS_STATUS_SUCCESS) {                                             \
-            set_error("linear: %s failed (%s)", what, status_text(s_));                \
-            return 1;                                                                   \
-        }                                                                               \
-    } while (0)
-
-int make_plan(GemmDevice& g, const GemmKey& k, const float* bias, GemmPlan* out) {
-    GemmPlan p;
-    // Column-major view of the row-major product y[rows, N] = x[rows, K] W[N, K]^T:
-    // y^T (N x rows, ld N) = op_T(W as K x N, ld K) * (x^T as K x rows, ld K).
-    KVP_LT(hipblasLtMatmulDescCreate(&p.desc, HIPBLAS_COMPUTE_32F, HIP_R_32F), "desc create");
-    const int32_t opa = HIPBLAS_OP_T, opb = HIPBLAS_OP_N;
-    KVP_LT(hipblasLtMatmulDescSetAttribute(p.desc, HIPBLASLT_MATMUL_DESC_TRANSA, &opa, sizeof(opa)),
-           "transA");
-    KVP_LT(hipblasLtMatmulDescSetAttribute(p.desc, HIPBLASLT_MATMUL_DESC_TRANSB, &opb, sizeof(opb)),
-           "transB");
-    if (k.bias) {
-        const uint32_t epi = HIPBLASLT_EPILOGUE_BIAS;
-        const int32_t bt = HIP_R_32F;
-        KVP_LT(hipblasLtMatmulDescSetAttribute(p.desc, HIPBLASLT_MATMUL_DESC_EPILOGUE, &epi,
-                                               sizeof(epi)),
-               "epilogue");
-        KVP_LT(hipblasLtMatmulDescSetAttribute(p.desc, HIPBLASLT_MATMUL_DESC_BIAS_DATA_TYPE, &bt,
-                                               sizeof(bt)),
-               "bias type");
-        KVP_LT(hipblasLtMatmulDescSetAttribute(p.desc, HIPBLASLT_MATMUL_DESC_BIAS_POINTER, &bias,
-                                               sizeof(bias)),
-               "bias pointer");
-    }
-    KVP_LT(hipblasLtMatrixLayoutCreate(&p.la, hip_type(k.in_t), (uint64_t)k.K, (uint64_t)k.N,
-                                       (int64_t)k.K),
-           "layout W");
-    KVP_LT(hipblasLtMatrixLayoutCreate(&p.lb, hip_type(k.in_t), (uint64_t)k.K, (uint64_t)k.rows,
-                                       (int64_t)k.K),
-           "layout x");
-    KVP_LT(hipblasLtMatrixLayoutCreate(&p.lc, hip_type(k.out_t), (uint64_t)k.N, (uint64_t)k.rows,
-                                       (int64_t)k.N),
-           "layout y");
-    hipblasLtMatmulPreference_t pref = nullptr;
-    KVP_LT(hipblasLtMatmulPreferenceCreate(&pref), "preference create");
-    const uint64_t maxws = kGemmWorkspace;
-    KVP_LT(hipblasLtMatmulPreferenceSetAttribute(pref, HIPBLASLT_MATMUL_PREF_MAX_WORKSPACE_BYTES,
-                                                 &maxws, sizeof(maxws)),
-           "preference workspace");
-    hipblasLtMatmulHeuristicResult_t res[1];
-    int count = 0;
-    const hipblasStatus_t hs = hipblasLtMatmulAlgoGetHeuristic(g.handle, p.desc, p.la, p.lb, p.lc,
-                                                               p.lc, pref, 1, res, &count);
-    hipblasLtMatmulPreferenceDestroy(pref);
-    if (hs != HIPBLAS_STATUS_SUCCESS || count < 1) {
-        set_error("linear: no hipBLASLt algorithm for in_dtype=%d out_dtype=%d rows=%ld K=%d N=%d "
-                  "accumulate=%d (%s)",
-                  k.in_t, k.out_t, k.rows, k.K, k.N, k.acc, status_text(hs));
-        return 1;
-    }
-    p.algo = res[0].algo;
-    p.ws = res[0].workspaceSize;
-    *out = p;
-    return 0;
-}
 
 int linear_impl(int in_t, int out_t, const void* x, const void* w, const float* bias, void* y,
                 long rows, int K, int N, bool acc, void* stream) {
-    if (!((in_t == 0 && out_t == 0) || (in_t == 1 && (out_t == 0 || out_t == 1)))) {
-        set_error("linear: dtype pair (%d, %d) not supported (fp32->fp32, bf16->bf16, "
-                  "bf16->fp32)",
-                  in_t, out_t);
-        return 1;
+    if (in_t == 1 && K % 64 == 0 && N % 128 == 0 && aligned16(x) && aligned16(w) &&
+        aligned16(bias) && aligned16(y) && rows > 0 && (out_t == 0 || !acc)) {
+        void* outs[3] = {y, nullptr, nullptr};
+        const int rc = launch_proj_gemm(x, w, bias, outs, 1, rows, K, N, out_t, acc, 128, stream);
+        if (rc != 2) return rc;
+        clear_error();
     }
-    if (rows <= 0 || K <= 0 || N <= 0) {
-        set_error("linear: empty shape rows=%ld in=%d out=%d", rows, K, N);
-        return 1;
-    }
-    if (!x || !w || !y) {
-        set_error("linear: null x/w/y pointer");
-        return 1;
-    }
-    const int dev = [] {
-        int d = 0;
-        return hipGetDevice(&d) == hipSuccess ? d : -1;
-    }();
-    if (dev < 0) {
-        set_error("linear: no HIP device available");
-        return 1;
-    }
-    std::lock_guard<std::mutex> lk(g_gemm_mu);
-    if ((int)g_gemm.size() <= dev) g_gemm.resize(dev + 1, nullptr);
-    if (!g_gemm[dev]) g_gemm[dev] = new GemmDevice();
-    GemmDevice& g = *g_gemm[dev];
-    if (!g.handle) KVP_LT(hipblasLtCreate(&g.handle), "handle create");
-    const GemmKey key{in_t, out_t, rows, K, N, acc ? 1 : 0, bias ? 1 : 0};
-    auto it = g.plans.find(key);
-    if (it == g.plans.end()) {
-        GemmPlan p;
-        if (make_plan(g, key, bias, &p)) return 1;
-        it = g.plans.emplace(key, p).first;
-    }
-    GemmPlan& p = it->second;
-    if (bias)
-        KVP_LT(hipblasLtMatmulDescSetAttribute(p.desc, HIPBLASLT_MATMUL_DESC_BIAS_POINTER, &bias,
-                                               sizeof(bias)),
-               "bias pointer");
-    StreamWorkspace& sw = g.ws[stream];
-    if (sw.bytes < p.ws) {
-        if (sw.ptr) {
-            (void)hipStreamSynchronize(static_cast<hipStream_t>(stream));
-            (void)hipFree(sw.ptr);
-            sw.ptr = nullptr;
-            sw.bytes = 0;
-        }
-        if (hipMalloc(&sw.ptr, p.ws) != hipSuccess) {
-            sw.ptr = nullptr;
-            set_error("linear: workspace allocation of %zu bytes failed", p.ws);
-            return 1;
-        }
-        sw.bytes = p.ws;
-    }
-    const float alpha = 1.f, beta = acc ? 1.f : 0.f;
-    KVP_LT(hipblasLtMatmul(g.handle, p.desc, &alpha, w, p.la, x, p.lb, &beta, y, p.lc, y, p.lc,
-                           &p.algo, sw.ptr, sw.bytes, static_cast<hipStream_t>(stream)),
-           "matmul");
-    return launch_ok("linear");
+    return launch_gemm_generic(in_t, out_t, x, w, bias, y, rows, K, N, acc, stream);
 }
 
 int layer_norm_impl(int in_t, int out_t, const void* x, const float* gamma, const float* beta,
@@ -459,7 +299,7 @@ int qkv_project_impl(int dtype, const float* x, const float* ln_w, const float* 
         void* outs[3] = {q, k, v};
         const int rc = launch_proj_gemm(xn, w_qkv, b_qkv, outs, 3, rows, D, D, 1, false, 128,
                                         stream);
-        if (rc != 2) return rc;  // 2: shape outside the kernel's tiling, use hipBLASLt
+        if (rc != 2) return rc;  // 2: shape outside the kernel's tiling: generic kernel
         clear_error();
     }
     const size_t es = dtype_size(dtype);

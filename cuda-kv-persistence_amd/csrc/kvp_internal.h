@@ -120,5 +120,11 @@ int fill_words(void* dst, long n, unsigned value, void* stream);
 int launch_proj_gemm(const void* x, const void* w, const float* bias, void* const* outs,
                      int groups, long rows, int K, int Ng, int out_dtype, bool accumulate,
                      int tile_n, void* stream);
+// Any-shape linear layer (proj_gemm.hip, fp32 matrix cores):
+// y[r, n] = sum_k x[r, k] w[n, k] + bias[n] (+ y[r, n] when accumulate, fp32
+// output only); in/out dtype pairs fp32->fp32, bf16->bf16, bf16->fp32.
+int launch_gemm_generic(int in_dtype, int out_dtype, const void* x, const void* w,
+                        const float* bias, void* y, long rows, int K, int N, bool accumulate,
+                        void* stream);
 
 }  // namespace kvp

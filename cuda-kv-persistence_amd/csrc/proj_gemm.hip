@@ -480,11 +480,31 @@ __global__ __launch_bounds__(kPThreads, 2) void proj_gemm_bf16_small_kernel(Proj
     constexpr int kChunks = kFeat * kEs / 16;
     constexpr int kRowsPerPass = 64 / kChunks;
     static_assert(4 * 32 * kRowB <= 2 * kSB, "staging exceeds LDS");
-    pj_barrier();
     OutT* out = static_cast<OutT*>(a.out[g]);
-    unsigned char* sbase = lds + wave * 32 * kRowB;
     const int rchunk = lane % kChunks;
     const int rrow = lane / kChunks;
+    // Accumulating (out_proj into the fp32 residual stream): every residual
+    // value the wave adds is loaded first, all at once, so the loads overlap
+    // one another and the staging below (loaded pass by pass, each add waited
+    // for its own load: 2 x 8 round trips to memory per wave at the end of
+    // every tile).
+    constexpr int kPasses = 32 / kRowsPerPass;
+    float4 resid[kAcc ? JR : 1][kAcc ? kPasses : 1];
+    if constexpr (kAcc) {
+#pragma unroll
+        for (int j = 0; j < JR; ++j) {
+#pragma unroll
+            for (int pass = 0; pass < kPasses; ++pass) {
+                const long r = r0 + wr * (TR / 2) + 32 * j + pass * kRowsPerPass + rrow;
+                const float* gp = reinterpret_cast<const float*>(out) + r * a.Ng + n0 +
+                                  wn * kFeat + 4 * rchunk;
+                resid[j][pass] = r < a.rows ? *reinterpret_cast<const float4*>(gp)
+                                            : make_float4(0.f, 0.f, 0.f, 0.f);
+            }
+        }
+    }
+    pj_barrier();
+    unsigned char* sbase = lds + wave * 32 * kRowB;
 #pragma unroll
     for (int j = 0; j < JR; ++j) {
         unsigned char* wrow = sbase + lq * kRowB;
@@ -520,7 +540,7 @@ __global__ __launch_bounds__(kPThreads, 2) void proj_gemm_bf16_small_kernel(Proj
             unsigned char* gp = reinterpret_cast<unsigned char*>(out + r * a.Ng + n0 + wn * kFeat) +
                                 16 * rchunk;
             if constexpr (kAcc) {
-                float4 y = *reinterpret_cast<const float4*>(gp);
+                float4 y = resid[j][pass];
                 y.x += __uint_as_float(vals[0]);
                 y.y += __uint_as_float(vals[1]);
                 y.z += __uint_as_float(vals[2]);
@@ -547,6 +567,163 @@ void launch_small(const ProjArgs& a, hipStream_t st) {
                        dim3((unsigned)grid), dim3(kPThreads), 0, st, a);
 }
 
+
+// ---------------------------------------------------------------------------
+// Generic linear layer (shapes the grouped kernel does not tile, and fp32):
+//
+//   y[r, n] = sum_k x[r, k] * w[n, k] + bias[n]  (+ y[r, n])
+//
+// x [rows, K], w [N, K] row-major (K-contiguous), fp32 or bf16 (widened to
+// fp32 in LDS), bias fp32 or null, y fp32 or bf16 (fp32 may accumulate into
+// itself). fp32 matrix cores: v_mfma_f32_32x32x2_f32 (full fp32 products,
+// fp32 accumulation). Workgroup = 4 waves, output tile 64 features x 64
+// rows, wave (w & 1, w >> 1) owns 32 x 32 of it: lane l holds row (l % 32)
+// of the block and features 8*(v/4) + 4*(l/32) + v%4 in accumulator v (A =
+// w rows, B = x rows, as in the grouped kernel). K advances in chunks of 32;
+// each chunk of w and x is staged in LDS as 64 rows of 32 values padded to
+// 33, so that the 32 lanes of a half-wave reading one k of 32 rows hit 32
+// distinct banks. Every global access is bounds-checked: any rows, K and N.
+// ---------------------------------------------------------------------------
+constexpr int kGTile = 64;
+constexpr int kGChunk = 32;
+constexpr int kGPitch = kGChunk + 1;
+
+struct GenericArgs {
+    const void* x;
+    const void* w;
+    const float* bias;
+    void* y;
+    long rows;
+    int K, N;
+    int n_tiles;
+};
+
+template <typename T>
+__device__ __forceinline__ float to_f32(T v) {
+    return (float)v;
+}
+
+template <typename InT, typename OutT, bool kAcc>
+__global__ __launch_bounds__(256) void gemm_generic_kernel(GenericArgs a) {
+    __shared__ float ws[kGTile * kGPitch];
+    __shared__ float xs[kGTile * kGPitch];
+    const int tid = threadIdx.x;
+    const int wave = tid >> 6;
+    const int lane = tid & 63;
+    const long n0 = (long)(blockIdx.x % a.n_tiles) * kGTile;
+    const long r0 = (long)(blockIdx.x / a.n_tiles) * kGTile;
+    const InT* W = static_cast<const InT*>(a.w);
+    const InT* X = static_cast<const InT*>(a.x);
+    const int bn = 32 * (wave & 1);   // the wave's feature block within the tile
+    const int br = 32 * (wave >> 1);  // its row block
+    const int lr = lane & 31;
+    const int lk = lane >> 5;
+    f32x16 acc;
+#pragma unroll
+    for (int v = 0; v < 16; ++v) acc[v] = 0.f;
+    for (int k0 = 0; k0 < a.K; k0 += kGChunk) {
+        // 64 rows x 32 k of each operand: element e = tid + 256 j is row
+        // e / 32, k e % 32 (a warp's consecutive lanes read consecutive k)
+#pragma unroll
+        for (int j = 0; j < kGTile * kGChunk / 256; ++j) {
+            const int e = tid + 256 * j;
+            const int row = e / kGChunk;
+            const int kk = e % kGChunk;
+            const long gk = (long)k0 + kk;
+            const long gn = n0 + row;
+            const long gr = r0 + row;
+            ws[row * kGPitch + kk] = gn < a.N && gk < a.K ? to_f32(W[gn * a.K + gk]) : 0.f;
+            xs[row * kGPitch + kk] = gr < a.rows && gk < a.K ? to_f32(X[gr * a.K + gk]) : 0.f;
+        }
+        __syncthreads();
+#pragma unroll
+        for (int kk = 0; kk < kGChunk; kk += 2) {
+            const float av = ws[(bn + lr) * kGPitch + kk + lk];
+            const float bv = xs[(br + lr) * kGPitch + kk + lk];
+            acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av, bv, acc, 0, 0, 0);
+        }
+        __syncthreads();
+    }
+    const long r = r0 + br + lr;
+    if (r >= a.rows) return;
+    OutT* Y = static_cast<OutT*>(a.y) + r * a.N;
+#pragma unroll
+    for (int v = 0; v < 16; ++v) {
+        const long n = n0 + bn + 8 * (v / 4) + 4 * lk + v % 4;
+        if (n >= a.N) continue;
+        float val = acc[v] + (a.bias ? a.bias[n] : 0.f);
+        if constexpr (kAcc) val += to_f32(Y[n]);
+        Y[n] = (OutT)val;
+    }
+}
+
+template <typename InT, typename OutT, bool kAcc>
+void launch_generic(const GenericArgs& a, long grid, hipStream_t st) {
+    hipLaunchKernelGGL((gemm_generic_kernel<InT, OutT, kAcc>), dim3((unsigned)grid), dim3(256), 0,
+                       st, a);
+}
+
+}  // namespace
+
+int launch_gemm_generic(int in_dtype, int out_dtype, const void* x, const void* w,
+                        const float* bias, void* y, long rows, int K, int N, bool accumulate,
+                        void* stream) {
+    if (!((in_dtype == 0 && out_dtype == 0) || (in_dtype == 1 && (out_dtype == 0 || out_dtype == 1)))) {
+        set_error("linear: dtype pair (%d, %d) not supported (fp32->fp32, bf16->bf16, "
+                  "bf16->fp32)",
+                  in_dtype, out_dtype);
+        return 1;
+    }
+    if (rows <= 0 || K <= 0 || N <= 0) {
+        set_error("linear: empty shape rows=%ld in=%d out=%d", rows, K, N);
+        return 1;
+    }
+    if (accumulate && out_dtype != 0) {
+        set_error("linear: accumulate needs fp32 output");
+        return 1;
+    }
+    if (!x || !w || !y) {
+        set_error("linear: null x/w/y pointer");
+        return 1;
+    }
+    GenericArgs a;
+    a.x = x;
+    a.w = w;
+    a.bias = bias;
+    a.y = y;
+    a.rows = rows;
+    a.K = K;
+    a.N = N;
+    const long n_tiles = ((long)N + kGTile - 1) / kGTile;
+    const long r_tiles = (rows + kGTile - 1) / kGTile;
+    if (n_tiles * r_tiles > 0x7fffffffL) {
+        set_error("linear: grid too large");
+        return 1;
+    }
+    a.n_tiles = (int)n_tiles;
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    const long grid = n_tiles * r_tiles;
+    if (in_dtype == 0) {
+        if (accumulate)
+            launch_generic<float, float, true>(a, grid, st);
+        else
+            launch_generic<float, float, false>(a, grid, st);
+    } else if (out_dtype == 1) {
+        launch_generic<__bf16, __bf16, false>(a, grid, st);
+    } else if (accumulate) {
+        launch_generic<__bf16, float, true>(a, grid, st);
+    } else {
+        launch_generic<__bf16, float, false>(a, grid, st);
+    }
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) {
+        set_error("linear launch: %s", hipGetErrorString(e));
+        return 1;
+    }
+    return 0;
+}
+
+namespace {
 }  // namespace
 
 int launch_proj_gemm(const void* x, const void* w, const float* bias, void* const* outs,

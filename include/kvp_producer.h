@@ -31,9 +31,12 @@ int kvp_layer_norm(int in_dtype, int out_dtype, const void* x,
                    int D, float eps, void* stream);
 
 /* nn.Linear (reference: src/backbone.py:13-14,44):
- * y[rows, out] = x[rows, in] W[out, in]^T + bias (+ y when accumulate != 0).
- * W has the storage dtype of x; bias fp32 [out] or NULL.
- * (in_dtype, out_dtype): (0, 0), (1, 1) or (1, 0). */
+ * y[rows, out] = x[rows, in] W[out, in]^T + bias (+ y when accumulate != 0,
+ * fp32 output only). W has the storage dtype of x; bias fp32 [out] or NULL.
+ * (in_dtype, out_dtype): (0, 0), (1, 1) or (1, 0). Any shape: bf16 shapes
+ * with in % 64 == 0, out % 128 == 0 and 16-byte aligned operands run on the
+ * grouped projection kernel (kvp_proj_gemm), every other shape and fp32 on
+ * this library's generic fp32-matrix-core kernel; no library GEMM. */
 int kvp_linear(int in_dtype, int out_dtype, const void* x, const void* w,
                const float* bias, void* y, long rows, int in_features,
                int out_features, int accumulate, void* stream);

@@ -117,8 +117,13 @@ def test_config_and_constructor_mirror_reference():
 @pytest.mark.parametrize("in_dt,out_dt,acc", [(0, 0, False), (0, 0, True), (1, 1, False),
                                               (1, 0, True), (1, 0, False)])
 @pytest.mark.parametrize("rows,K,N,bias", [(1, 16, 1536, True), (77, 256, 384, True),
-                                           (1560, 1536, 1536, True), (300, 1536, 1536, False)])
+                                           (1560, 1536, 1536, True), (300, 1536, 1536, False),
+                                           (130, 100, 77, True), (65, 192, 200, False),
+                                           (3, 1536, 1535, True)])
 def test_linear_matches_oracle(in_dt, out_dt, acc, rows, K, N, bias):
+    """Shapes the grouped bf16 kernel tiles (K % 64, N % 128) run on it, every
+    other shape and fp32 on the generic fp32-matrix-core kernel; both within
+    1e-4 (fp32 out) or one bf16 ulp of the oracle."""
     print(f"linear in={in_dt} out={out_dt} acc={acc} rows={rows} K={K} N={N}", flush=True)
     rng = np.random.default_rng(rows + K + N)
     x = rng.standard_normal((rows, K)).astype(np.float32)
