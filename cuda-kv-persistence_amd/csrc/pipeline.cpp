@@ -23,15 +23,21 @@
 //     host for every frame first (a bookkeeping-only manager takes the same
 //     decisions: which rows each frame maps); then one staging launch and one
 //     attention launch cover every frame. K and V are fixed for the whole
-//     layer, so a row holds the same bytes in every frame that maps it: the
-//     layer arena holds each row mapped by any frame once (physical rows in
-//     first-mapped order), and frame f's slice of the layer map points each
-//     of its mapped rows at that row's physical row. The staging launch
-//     copies each such row once, as runs of consecutive rows, and writes the
-//     map entries that differ from the previous run, as runs. Every frame
-//     maps exactly the rows the single arena maps at that frame, holding the
-//     same bytes, so the outputs are those of frame-by-frame stepping, bit for
-//     bit; only the arena placement differs (physical rows, not slots).
+//     layer, so a row holds the same bytes in every frame that maps it. The
+//     layer arena gives each tile that some frame maps physical rows for the
+//     longest prefix of it that any frame maps, whole tiles in key order, and
+//     frame f's slice of the layer map points each of its mapped rows at
+//     that row's physical row. The staging launch copies those tile prefixes
+//     (as runs of consecutive rows), writes the map entries that differ from
+//     the previous run (as runs) and, in bf16, the changed group-descriptor
+//     entries of every slice. The arena is allocated once, at frames x the
+//     rows of the set-aside (no frame maps more), and never grows; a plan past
+//     it is an error. Every frame maps exactly the rows the single arena maps
+//     at that frame, holding the same bytes: outputs are bitwise equal across
+//     policies and modes within kvp_pipeline_run, and equal stepping's up to
+//     the rounding of stepping's key split (the layer launch never splits).
+//     A failure after the layer state was touched tears it down, and the
+//     next run rebuilds it from scratch.
 // Nothing synchronises the host per frame; all device work is ordered on the
 // pipeline's stream.
 
