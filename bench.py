@@ -6,8 +6,9 @@ Workload "C3", the configuration of the headline metric: Wan2.1-1.3B shape,
 (drawn on the device, seed 42 + layer), causal cross-frame attention, motion
 scores from a seeded smooth AR(1) field. One step = the whole 30-layer pass
 of the gated pipeline: per layer, every frame's policy select and arena
-plan on the host, one staging launch (every frame's arena region and KVMap
-slice), one attention launch over all 8 frames; all stream-ordered.
+plan on the host, one staging launch (the shared layer arena, every
+frame's KVMap slice and descriptor table), one attention launch over all 8
+frames; all stream-ordered.
 
 value = ms per query frame of that step (all 30 layers), policy `motion`
 (override with --policy, workload with --config c4 / c5).
@@ -24,6 +25,14 @@ scale of FETCH_SIZE / WRITE_SIZE. `roofline` is the dominant kernel's
 (attn_fwd_bf16, the headline policy's instantiation). `cpu_baseline` is the
 oracle's PyTorch fp32 attention on a bounded sample on this host's cores.
 `c4` / `c5` objects: the other multi-frame configurations, motion policy.
+
+The map-free kernel (policy none) and the descriptor kernel (the gated
+policies) differ in fabric reads even where the descriptor kernel reads no
+arena row, because their per-tile timing keeps an XCD's workgroups in step
+differently. So the same quantities are also reported for policy none run
+through the descriptor kernel with an empty table (`none_descriptor_kernel`),
+with every gated policy's time and read delta against it (`..._same_kernel`):
+the arena's own effect.
 
 Also reported under "kv_producer": the upstream K/V producer (the reference's
 DiT backbone forward, src/backbone.py:8-67) at the C3 frame set, whole
@@ -461,6 +470,12 @@ def motion_cpu_baseline(frames):
 
 
 POLICIES = ("none", "uniform", "recency", "motion", "reuse_weighted")
+# Policy none run through the gated policies' kernel instantiation (group
+# descriptors) with an empty table: it reads exactly the rows the map-free
+# kernel reads and computes the same output, so gated policies measured
+# against it show the arena's own effect on time and bytes, apart from the
+# instantiation's.
+SAME_KERNEL = "none_descriptor_kernel"
 ATTN_KERNEL = "attn_fwd_bf16_kernel"
 # a split launch's combine belongs to its attention launch (frame-by-frame
 # mode only; the layer launch never splits)
@@ -469,6 +484,27 @@ STAGE_KERNELS = ("stage_kernel", "stage_runs_kernel", "map_fill_kernel", "fill_w
 COPY_KERNEL = "__amd_rocclr_copyBuffer"
 CALIB_BYTES = 256 << 20
 CALIB_COPIES = 4
+
+
+def empty_table_launcher(torch, api, workloads, c, stream):
+    """The layer launch of policy none through the descriptor instantiation
+    (kvp_attn_forward_frames_gd): every KVMap entry -1, every descriptor
+    entry "no arena row", a one-row arena that is never read. Returns
+    launch(q, k, v, out) on `stream`."""
+    F, T, W = c.frames, c.tokens, c.window
+    D, H = workloads.HIDDEN, workloads.HEADS
+    span = F * T
+    longest = (min(W, F) if W else F) * T
+    n = 4 * ((longest + 63) // 64)
+    kvmap = torch.full((F * span,), -1, dtype=torch.int64, device="cuda")
+    gd = torch.zeros((F * n * 2,), dtype=torch.int32, device="cuda")
+    arena = torch.zeros((1, 2 * D), dtype=torch.bfloat16, device="cuda")
+
+    def launch(q, k, v, out):
+        api.attn_forward_frames_gd(q, k, v, arena, kvmap, gd, out, F, T, D, H, cross=True,
+                                   window_frames=W, map_frame_stride=span, gd_frame_stride=n,
+                                   stream=stream)
+    return launch
 
 
 def counter_run(counters, policy, args, workdir, config=None, step_mode=False, layers=None):
@@ -579,6 +615,17 @@ def counter_set(args, work, config, policies, frames_total, *, write_policy=None
             rec["all_kernels_read_delta_vs_none"] = round(
                 rec["all_kernels_read_bytes_per_frame"]
                 / base["all_kernels_read_bytes_per_frame"] - 1.0, 5)
+    same = res["policies"].get(SAME_KERNEL)
+    if same:
+        # the arena's own effect: gated policies against none on their kernel
+        for pol, rec in res["policies"].items():
+            if pol not in ("none", SAME_KERNEL):
+                rec["attn_read_delta_vs_none_same_kernel"] = round(
+                    rec["attn_read_bytes_per_frame"] / same["attn_read_bytes_per_frame"] - 1.0,
+                    5)
+                rec["all_kernels_read_delta_vs_none_same_kernel"] = round(
+                    rec["all_kernels_read_bytes_per_frame"]
+                    / same["all_kernels_read_bytes_per_frame"] - 1.0, 5)
     return res
 
 
@@ -597,7 +644,8 @@ def measure_counters(args, cfg, headline):
     t0 = time.perf_counter()
     out = {}
     with tempfile.TemporaryDirectory(prefix="kvp_bench_") as work:
-        head = counter_set(args, work, args.config, POLICIES, args.layers * cfg.frames,
+        head = counter_set(args, work, args.config, POLICIES + (SAME_KERNEL,),
+                           args.layers * cfg.frames,
                            write_policy=headline, hit_policies=("none", headline))
         out["policies"] = head["policies"]
         out["counter_runs"] = head["runs"]
@@ -607,7 +655,8 @@ def measure_counters(args, cfg, headline):
         out["counter_runs"] += step["runs"]
         if not args.no_legs:
             legs = {}
-            for name, pols in (("c4", POLICIES), ("c5", ("none", "motion"))):
+            for name, pols in (("c4", POLICIES + (SAME_KERNEL,)),
+                               ("c5", ("none", "motion", SAME_KERNEL))):
                 if name == args.config:
                     continue
                 c = workloads.CONFIGS[name]
@@ -770,6 +819,20 @@ def main():
         wall = (time.perf_counter() - t0) * 1e3
         return e0.elapsed_time(e1) / steps, wall / steps
 
+    def same_kernel_pass(data, launch):
+        """HIP events around every layer's launch of `launch` (the empty-table
+        descriptor launch), as attn_pass; returns ms per layer."""
+        evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+               for _ in data]
+        scratch = torch.empty_like(data[0][3])
+        for rep in range(2):
+            for (q, k, v, _, _), (a, b) in zip(data, evs):
+                a.record()
+                launch(q, k, v, scratch)
+                b.record()
+            torch.cuda.synchronize()
+        return sum(a.elapsed_time(b) for a, b in evs) / len(evs)
+
     def attn_pass(c, pl, data, gated):
         """HIP events around every layer's attention launch: the pipeline's own
         launch (kvp_pipeline_layer_attention, on its stream) with the layer
@@ -791,6 +854,18 @@ def main():
     data = workload(cfg)
     log(f"inputs resident ({args.config})")
 
+    if args.profile_policy == SAME_KERNEL:
+        # policy none's 30 layer launches through the descriptor
+        # instantiation with an empty table, then the calibration copies
+        launch = empty_table_launcher(torch, api, workloads, cfg, stream)
+        for q, k, v, out, _ in data:
+            launch(q, k, v, out)
+        torch.cuda.synchronize()
+        if args.calibrate:
+            calibration_copies()
+        print(json.dumps({"profile_policy": SAME_KERNEL, "config": args.config,
+                          "layers": layers, "frames": cfg.frames}), flush=True)
+        return
     if args.profile_policy:
         # one step (what the rocprofv3 passes count), then the calibration
         # copies; --steps > 1 also times steps 2.. (outside the profiler only)
@@ -862,6 +937,30 @@ def main():
         log(f"policy {pol}: {t / F:.4f} ms/frame, attention alone {lay_ms * layers / F:.4f} "
             f"ms/frame ({tf:.0f} TFLOP/s)")
 
+    # --- policy none on the gated policies' kernel (descriptor instantiation,
+    # empty table): separates the arena's own effect from the instantiation's
+    same_ms = same_kernel_pass(data, empty_table_launcher(torch, api, workloads, cfg, stream))
+    same_out = torch.empty_like(data[0][3])
+    empty_table_launcher(torch, api, workloads, cfg, stream)(*data[0][:3], same_out)
+    torch.cuda.synchronize()
+    tf = fl_layer / (same_ms * 1e-3) / 1e12
+    rec = {"what": "policy none through the descriptor instantiation with an empty table "
+                   "(no arena row read, the map-free kernel's arithmetic)",
+           "bitwise_equal_to_none": bool(torch.equal(same_out, ref_out)),
+           "attn_kernel_ms_per_frame": round(same_ms * layers / F, 4),
+           "attn_kernel_ms_per_layer_launch": round(same_ms, 5),
+           "attn_tflops": round(tf, 2), "attn_mfma_frac": round(tf / BF16_PEAK_TFLOPS, 4)}
+    c = (counters or {}).get("policies", {}).get(SAME_KERNEL)
+    if c:
+        rec.update(c)
+        rec["attn_read_vs_compulsory"] = round(c["attn_read_bytes_per_frame"] / comp_frame, 4)
+    policies[SAME_KERNEL] = rec
+    for pol in POLICIES[1:]:
+        policies[pol]["attn_time_delta_vs_none_same_kernel"] = round(
+            policies[pol]["attn_kernel_ms_per_layer_launch"] / same_ms - 1.0, 5)
+    log(f"none on the descriptor kernel: attention alone {same_ms * layers / F:.4f} ms/frame "
+        f"({tf:.0f} TFLOP/s)")
+
     # --- reference-exact leg: the same layers frame by frame (kvp_pipeline_step:
     # the reference driver's sequence, one arena of set_aside bytes refilled per
     # frame, the reference's slot layout and KVMap values, one attention launch
@@ -908,6 +1007,9 @@ def main():
             t, _ = timed(pl, data_leg, 2)
             lm = attn_pass(c, pl, data_leg, True)
             tfl = c.flops_per_layer() / (lm * 1e-3) / 1e12
+            # policy none on the same instantiation (empty table), first 10 layers
+            lm_same = same_kernel_pass(data_leg[:10], empty_table_launcher(
+                torch, api, workloads, c, stream))
             nb = FramePipeline("none", cross=True, streaming=False, frames=c.frames,
                                T=c.tokens, D=workloads.HIDDEN, heads=workloads.HEADS,
                                dtype=api.BF16, window_frames=c.window)
@@ -924,6 +1026,8 @@ def main():
                 "pipeline_ms_per_frame": round(t / c.frames, 4),
                 "attn_kernel_ms_per_frame": round(lm * layers / c.frames, 4),
                 "attn_tflops": round(tfl, 2), "attn_mfma_frac": round(tfl / BF16_PEAK_TFLOPS, 4),
+                "none_same_kernel_attn_ms_per_frame": round(lm_same * layers / c.frames, 4),
+                "attn_time_delta_vs_none_same_kernel": round(lm / lm_same - 1.0, 5),
                 "attn_launches_per_layer": 1, "key_splits": 1,
                 "bitwise_equal_to_none_layer0": bool(torch.equal(o_motion, out)),
                 "layer_arena_alloc_bytes": pl.layer_arena_bytes(),
