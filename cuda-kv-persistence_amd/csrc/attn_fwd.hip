@@ -1010,7 +1010,7 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_bf16_kernel(AttnArgs a) 
 
     // ---- copies of a descriptor launch (kGd) ----
     // Copy i of a wave moves rows 4i..4i+3 of its 16-row group (row
-    // gvidx[i] = 4i + (lane >> 4), chunk lane & 15, as in copy_plain) with
+    // 4i + (lane >> 4), chunk lane & 15, as in copy_plain) with
     // raw buffer loads whose lane offset is row x pitch + chunk: an original
     // row (pitch rb, descriptor based at the group's first row) or an arena
     // row ([K row | V row], pitch 2 rb, descriptor based at arena row l - r0
@@ -1020,9 +1020,14 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_bf16_kernel(AttnArgs a) 
     // x stride in the descriptor, need no per-copy lane arithmetic, but with
     // them the windowed launch read 25 % more fabric bytes per frame than
     // with these.)
-    unsigned gvidx[4];  // row of copy i in the group
+    // byte offset of copy i's row at the original pitch: row 4i +
+    // (lane >> 4) of the group, times rb; the arena pitch (2 rb) is this
+    // shifted left by one, so a copy's lane offset is one shift-and-add of a
+    // loop-invariant value (a per-copy row x pitch multiply is a quarter-rate
+    // VALU op)
+    unsigned grow[4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) gvidx[i] = (unsigned)(4 * i + (lane >> 4));
+    for (int i = 0; i < 4; ++i) grow[i] = (unsigned)(4 * i + (lane >> 4)) * rb;
     // the step being set up (prep_gd): its original rows, the arena sub-run
     // its copies may take, which of the 4 copies take it, and what the slow
     // path needs
@@ -1081,7 +1086,7 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_bf16_kernel(AttnArgs a) 
             const_cast<unsigned char*>(ar ? ga_k + rb : go_v), (short)0, nrec, kBufFlags);
         // (a select between precomputed offsets of both pitches put those
         // arrays in scratch memory)
-        const unsigned row = gvidx[i] * (ar ? 2u * rb : rb);
+        const unsigned row = grow[i] << (ar ? 1u : 0u);
         KVP_LDS void* kd = (KVP_LDS void*)(uintptr_t)(gkoff + 1024u * (unsigned)i);
         KVP_LDS void* vd = (KVP_LDS void*)(uintptr_t)(gvoff + 1024u * (unsigned)i);
         __builtin_amdgcn_raw_ptr_buffer_load_lds(rk, kd, 16, row + kofs[i], 0, 0, 0);
