@@ -37,6 +37,11 @@
 //                            slid down a strip of rows, parked in LDS 4 rows
 //                            at a time, sliding sums along runs of 2 columns;
 //                            then the regularised 2 x 2 solve in fp64.
+//   update_flow_ring_kernel  the same for winsize 15 (the reference's), with
+//                            each column's 15 window rows held in a register
+//                            ring, so that M is read once instead of twice,
+//                            and the next rows' loads in flight across each
+//                            horizontal pass.
 //   flow_cells_kernel        |flow| averaged over grid cells (one workgroup
 //                            per cell row), then tile_change_kernel: the mean
 //                            of each run of tile_tokens cells in fp64.
@@ -72,6 +77,12 @@ constexpr int kPeTileW = 64, kPeTileH = 16;
 constexpr int kBfBatch = 4;       // box filter: rows parked in LDS at a time
 constexpr int kBfRun = 2;         // box filter: output columns per sliding run
 constexpr int kBfTargetGroups = 2048;
+// register-ring box filter (update_flow_ring_kernel): window half-width it
+// serves (winsize 15), rows per workgroup bounds, target workgroups per launch
+constexpr int kBfRingHalf = 7;
+constexpr int kBfRingRows = 45;
+constexpr int kBfRingMinRows = 10;
+constexpr int kBfRingGroups = 1024;
 
 struct BlurTaps {
     int ksize;
@@ -425,6 +436,130 @@ __global__ __launch_bounds__(COLS) void update_flow_kernel(const float* __restri
             }
         }
         __syncthreads();
+    }
+}
+
+// The same box filter and solve for winsize 2*kM+1 with the window's rows
+// kept in registers. update_flow_kernel reads every value of M twice (when
+// its row enters a column's window and again when it leaves); here each
+// thread keeps the 2kM+1 rows of its column's window for the 5 planes in a
+// ring of registers, so the leaving row's values come from the ring and M is
+// read once per strip (plus the first window of each workgroup's rows). The
+// row loop is unrolled by the ring period, so every ring slot is a static
+// register; rows are parked in LDS kRB at a time (kRB divides the period)
+// for the horizontal pass. Only the first `ncols` threads load a column:
+// the host sizes the strips to the level's width. The running sums see the
+// same values in the same order as update_flow_kernel (fp64: entering row
+// added, leaving row subtracted), so both kernels give the same flow for
+// the same rows per workgroup.
+template <int COLS, int kM>
+__global__ __launch_bounds__(COLS) void update_flow_ring_kernel(const float* __restrict__ M, int w,
+                                                                int h, int ncols, int rows,
+                                                                double scale,
+                                                                float2* __restrict__ flow) {
+    constexpr int kW = 2 * kM + 1;  // window rows = ring period
+    constexpr int kRB = 5;          // rows parked in LDS per horizontal pass
+    static_assert(kW % kRB == 0, "the LDS batch must divide the ring period");
+    __shared__ float buf[kRB][5][COLS];
+    const int tw = ncols - 2 * kM;
+    const int X0 = blockIdx.x * tw;
+    const int Y0 = blockIdx.y * rows;
+    const int p = blockIdx.z;
+    const long P = (long)w * h;
+    const float* Mp = M + (long)p * 5 * P;
+    float2* Fp = flow + (long)p * P;
+    const int tid = threadIdx.x;
+    const bool col_ok = tid < ncols;
+    const int xc = min(max(X0 - kM + tid, 0), w - 1);
+    // ring slot j holds the column's values of the row that entered the
+    // window j rows (mod kW) after the workgroup's first window row
+    float ring[5][kW];
+    double vs[5] = {0.0, 0.0, 0.0, 0.0, 0.0};
+#pragma unroll
+    for (int j = 0; j < kW; ++j) {
+        const float* q = Mp + (long)min(max(Y0 - kM + j, 0), h - 1) * w + xc;
+#pragma unroll
+        for (int c = 0; c < 5; ++c) {
+            ring[c][j] = col_ok ? q[c * P] : 0.f;
+            vs[c] += ring[c][j];
+        }
+    }
+    const int yend = min(Y0 + rows, h);
+    const int xend = min(tw, w - X0);  // output columns of this strip
+    const int runs = (xend + kBfRun - 1) / kBfRun;
+    // values of the rows entering after output rows yb .. yb+kRB-1 (row
+    // y+kM+1 after row y), loaded one batch ahead: their loads stay in flight
+    // across the batch's horizontal pass (the barriers below wait for LDS
+    // only)
+    float ent[kRB][5];
+    auto load_entering = [&](int yb) {
+#pragma unroll
+        for (int r = 0; r < kRB; ++r) {
+            const int y = yb + r;
+            const float* qa = Mp + (long)min(y + kM + 1, h - 1) * w + xc;
+            const bool ok = col_ok && y + 1 < yend;
+#pragma unroll
+            for (int c = 0; c < 5; ++c) ent[r][c] = ok ? qa[c * P] : 0.f;
+        }
+    };
+    load_entering(Y0);
+    for (int yc = Y0; yc < yend; yc += kW) {
+#pragma unroll
+        for (int b = 0; b < kW / kRB; ++b) {
+            const int yb = yc + b * kRB;
+            if (yb >= yend) break;
+            const int nr = min(kRB, yend - yb);
+#pragma unroll
+            for (int r = 0; r < kRB; ++r) {
+                if (r < nr) {
+#pragma unroll
+                    for (int c = 0; c < 5; ++c) buf[r][c][tid] = (float)vs[c];
+                    if (yb + r + 1 < yend) {
+                        // row yb+r+kM+1 enters, row yb+r-kM (ring slot b*kRB + r) leaves
+#pragma unroll
+                        for (int c = 0; c < 5; ++c) {
+                            vs[c] += (double)ent[r][c] - (double)ring[c][b * kRB + r];
+                            ring[c][b * kRB + r] = ent[r][c];
+                        }
+                    }
+                }
+            }
+            load_entering(yb + kRB);
+            // LDS-only barrier: the entering rows' loads stay in flight
+            asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+            for (int j = tid; j < nr * runs; j += COLS) {
+                const int r = j / runs;
+                const int x0 = (j - r * runs) * kBfRun;
+                const int n = min(kBfRun, xend - x0);
+                float s[5][kBfRun];
+#pragma unroll
+                for (int c = 0; c < 5; ++c) {
+                    const float* v = &buf[r][c][x0];
+                    float a = 0.f;
+#pragma unroll
+                    for (int k = 0; k < kW; ++k) a += v[k];
+                    s[c][0] = a;
+#pragma unroll
+                    for (int i = 1; i < kBfRun; ++i) {
+                        if (i < n) a += v[i + 2 * kM] - v[i - 1];
+                        s[c][i] = a;
+                    }
+                }
+                float2* out = Fp + (long)(yb + r) * w + X0 + x0;
+#pragma unroll
+                for (int i = 0; i < kBfRun; ++i) {
+                    if (i < n) {
+                        const double g11 = s[0][i] * scale, g12 = s[1][i] * scale;
+                        const double g22 = s[2][i] * scale, h1 = s[3][i] * scale;
+                        const double h2 = s[4][i] * scale;
+                        const double idet = 1.0 / (g11 * g22 - g12 * g12 + 1e-3);
+                        out[i] = make_float2((float)((g11 * h2 - g12 * h1) * idet),
+                                             (float)((g22 * h1 - g12 * h2) * idet));
+                    }
+                }
+            }
+            asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+        }
     }
 }
 
@@ -782,12 +917,28 @@ int farneback_impl(const uint8_t* frames, long frame_stride, int nf, int W, int 
         const bool narrow = l.w + 2 * m <= 128 || l.w < 400;
         const int cols = narrow ? 128 : 256;
         const int strips = (l.w + cols - 2 * m - 1) / (cols - 2 * m);
+        // winsize 15 (the reference's): the register-ring kernel, strips
+        // trimmed to the level's width, up to kBfRingRows rows per workgroup
+        // (a multiple of its LDS batch) so that a launch has ~kBfRingGroups
+        const bool ring = m == kBfRingHalf;
+        const int ring_cols = (l.w + strips - 1) / strips + 2 * m;
         long want = ((long)l.h * strips * pairs + kBfTargetGroups - 1) / kBfTargetGroups;
         int rows = (int)std::min<long>(32, std::max<long>(kBfBatch, want));
         rows = (rows + kBfBatch - 1) / kBfBatch * kBfBatch;
+        if (ring) {
+            want = ((long)l.h * strips * pairs + kBfRingGroups - 1) / kBfRingGroups;
+            rows = (int)std::min<long>(kBfRingRows, std::max<long>(kBfRingMinRows, want));
+            rows = (rows + 4) / 5 * 5;
+        }
         const dim3 box_grid(strips, (l.h + rows - 1) / rows, pairs);
         for (int it = 0; it < iterations; ++it) {
-            if (narrow)
+            if (ring && narrow)
+                update_flow_ring_kernel<128, kBfRingHalf><<<box_grid, 128, 0, st>>>(
+                    M, l.w, l.h, ring_cols, rows, box_scale, fl);
+            else if (ring)
+                update_flow_ring_kernel<256, kBfRingHalf><<<box_grid, 256, 0, st>>>(
+                    M, l.w, l.h, ring_cols, rows, box_scale, fl);
+            else if (narrow)
                 update_flow_kernel<128><<<box_grid, 128, 0, st>>>(M, l.w, l.h, m, rows, box_scale,
                                                                    fl);
             else
