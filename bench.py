@@ -16,7 +16,7 @@ value = ms per query frame of that step (all 30 layers), policy `motion`
 Reported per policy (none / uniform / recency / motion / reuse_weighted):
 pipeline ms/frame; attention-kernel ms/frame, TFLOP/s and fraction of the
 dense bf16 MFMA peak (HIP events around each layer launch, on the launch
-stream); fabric read bytes per frame of the attention kernel and of all
+stream, the median of 5 passes over the layers); fabric read bytes per frame of the attention kernel and of all
 library kernels, their delta vs none, and GB/s with the fraction of HBM
 peak. The bytes come from rocprofv3 --pmc child runs of this same script
 (`--profile-policy P`), started before this process touches the GPU; each
@@ -819,35 +819,34 @@ def main():
         wall = (time.perf_counter() - t0) * 1e3
         return e0.elapsed_time(e1) / steps, wall / steps
 
-    def same_kernel_pass(data, launch):
-        """HIP events around every layer's launch of `launch` (the empty-table
-        descriptor launch), as attn_pass; returns ms per layer."""
+    def event_passes(data, launch, passes=5):
+        """HIP events around every layer's launch(q, k, v, out): one warm-up
+        pass over the layers, then `passes` timed passes; returns the median
+        over the passes of the mean ms per layer."""
         evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
                for _ in data]
         scratch = torch.empty_like(data[0][3])
-        for rep in range(2):
+        per_pass = []
+        for rep in range(passes + 1):
             for (q, k, v, _, _), (a, b) in zip(data, evs):
                 a.record()
                 launch(q, k, v, scratch)
                 b.record()
             torch.cuda.synchronize()
-        return sum(a.elapsed_time(b) for a, b in evs) / len(evs)
+            if rep:
+                per_pass.append(sum(a.elapsed_time(b) for a, b in evs) / len(evs))
+        return sorted(per_pass)[len(per_pass) // 2]
 
-    def attn_pass(c, pl, data, gated):
-        """HIP events around every layer's attention launch: the pipeline's own
-        launch (kvp_pipeline_layer_attention, on its stream) with the layer
-        arena, KVMap slices and group descriptors its last run left; returns
-        ms per layer."""
-        evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-               for _ in data]
-        scratch = torch.empty_like(data[0][3])
-        for rep in range(2):  # the first pass warms, the second is measured
-            for (q, k, v, _, _), (a, b) in zip(data, evs):
-                a.record()
-                pl.layer_attention(q, k, v, scratch)
-                b.record()
-            torch.cuda.synchronize()
-        return sum(a.elapsed_time(b) for a, b in evs) / len(evs)
+    def same_kernel_pass(data, launch):
+        """The empty-table descriptor launch of every layer, as attn_pass."""
+        return event_passes(data, launch)
+
+    def attn_pass(c, pl, data, gated, passes=5):
+        """The pipeline's own attention launch of every layer
+        (kvp_pipeline_layer_attention, on its stream) with the layer arena,
+        KVMap slices and group descriptors its last run left; ms per layer,
+        the median of `passes` passes."""
+        return event_passes(data, pl.layer_attention, passes)
 
     set_aside = (cfg.set_aside if args.set_aside_tiles is None
                  else args.set_aside_tiles * workloads.BF16_TILE_BYTES)
@@ -1005,11 +1004,13 @@ def main():
             pl = make(c, "motion", c.set_aside)
             run_step(pl, data_leg)
             t, _ = timed(pl, data_leg, 2)
-            lm = attn_pass(c, pl, data_leg, True)
+            # attention alone: the median of 3 passes over every layer (C5,
+            # 0.5 s a launch: over the first 10 layers)
+            lm = attn_pass(c, pl, data_leg[:10] if name == "c5" else data_leg, True, passes=3)
             tfl = c.flops_per_layer() / (lm * 1e-3) / 1e12
             # policy none on the same instantiation (empty table), first 10 layers
-            lm_same = same_kernel_pass(data_leg[:10], empty_table_launcher(
-                torch, api, workloads, c, stream))
+            lm_same = event_passes(data_leg[:10], empty_table_launcher(
+                torch, api, workloads, c, stream), passes=3)
             nb = FramePipeline("none", cross=True, streaming=False, frames=c.frames,
                                T=c.tokens, D=workloads.HIDDEN, heads=workloads.HEADS,
                                dtype=api.BF16, window_frames=c.window)
