@@ -837,9 +837,24 @@ def main():
                 per_pass.append(sum(a.elapsed_time(b) for a, b in evs) / len(evs))
         return sorted(per_pass)[len(per_pass) // 2]
 
-    def same_kernel_pass(data, launch):
-        """The empty-table descriptor launch of every layer, as attn_pass."""
-        return event_passes(data, launch)
+    def round_robin_passes(data, launches, passes=5):
+        """event_passes for several launch(q, k, v, out) functions, their
+        passes interleaved (one pass of each in turn, a warm-up pass first);
+        returns {name: median over the passes of the mean ms per layer}."""
+        evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+               for _ in data]
+        scratch = torch.empty_like(data[0][3])
+        per = {name: [] for name in launches}
+        for rep in range(passes + 1):
+            for name, launch in launches.items():
+                for (q, k, v, _, _), (a, b) in zip(data, evs):
+                    a.record()
+                    launch(q, k, v, scratch)
+                    b.record()
+                torch.cuda.synchronize()
+                if rep:
+                    per[name].append(sum(a.elapsed_time(b) for a, b in evs) / len(evs))
+        return {name: sorted(v)[len(v) // 2] for name, v in per.items()}
 
     def attn_pass(c, pl, data, gated, passes=5):
         """The pipeline's own attention launch of every layer
@@ -898,23 +913,39 @@ def main():
     fl_layer = cfg.flops_per_layer()
     comp_frame = compulsory_read_bytes_per_frame(cfg)
     policies = {}
+    pls = {}
     ref_out = None
     for pol in POLICIES:
         pl = main_pl if pol == args.policy else make(cfg, pol, set_aside)
+        pls[pol] = pl
         run_step(pl, data)
         t, _ = timed(pl, data, max(1, min(2, args.steps)))
         o0 = data[0][3].clone()
         if ref_out is None:
             ref_out = o0
-        lay_ms = attn_pass(cfg, pl, data, pol != "none")
+        policies[pol] = {"pipeline_ms_per_frame": round(t / F, 4),
+                         "bitwise_equal_to_none": bool(torch.equal(o0, ref_out)),
+                         "attn_kernel_reads_kvmap": pol != "none",
+                         "staged_tiles_last_frame": pl.staged_tiles()}
+        log(f"policy {pol}: {t / F:.4f} ms/frame")
+
+    # --- the attention launch alone: every policy's own launch (its layer
+    # arena and tables) and policy none through the descriptor instantiation
+    # with an empty table, timed round-robin so that no policy is measured
+    # later than another (the board's clock drifts over a run) --------------
+    same_launch = empty_table_launcher(torch, api, workloads, cfg, stream)
+    launches = {pol: pls[pol].layer_attention for pol in POLICIES}
+    launches[SAME_KERNEL] = same_launch
+    alone = round_robin_passes(data, launches)
+    for pol in POLICIES:
+        pl = pls[pol]
+        lay_ms = alone[pol]
         tf = fl_layer / (lay_ms * 1e-3) / 1e12
-        rec = {"pipeline_ms_per_frame": round(t / F, 4),
-               "bitwise_equal_to_none": bool(torch.equal(o0, ref_out)),
-               "attn_kernel_ms_per_frame": round(lay_ms * layers / F, 4),
-               "attn_kernel_ms_per_layer_launch": round(lay_ms, 5),
-               "attn_tflops": round(tf, 2), "attn_mfma_frac": round(tf / BF16_PEAK_TFLOPS, 4),
-               "attn_kernel_reads_kvmap": pol != "none",
-               "staged_tiles_last_frame": pl.staged_tiles()}
+        rec = policies[pol]
+        rec.update({"attn_kernel_ms_per_frame": round(lay_ms * layers / F, 4),
+                    "attn_kernel_ms_per_layer_launch": round(lay_ms, 5),
+                    "attn_tflops": round(tf, 2),
+                    "attn_mfma_frac": round(tf / BF16_PEAK_TFLOPS, 4)})
         if pol != "none":
             # the layer arena: allocated once at frames x set-aside (the
             # reference's per-step arena summed over the frames), used by the
@@ -930,17 +961,16 @@ def main():
             rec["attn_read_gbs"] = round(gbs, 1)
             rec["attn_hbm_frac"] = round(gbs / HBM_PEAK_GBS, 4)
             rec["attn_read_vs_compulsory"] = round(c["attn_read_bytes_per_frame"] / comp_frame, 4)
-        policies[pol] = rec
         if pl is not main_pl:
             pl.close()
-        log(f"policy {pol}: {t / F:.4f} ms/frame, attention alone {lay_ms * layers / F:.4f} "
-            f"ms/frame ({tf:.0f} TFLOP/s)")
+        log(f"policy {pol}: attention alone {lay_ms * layers / F:.4f} ms/frame "
+            f"({tf:.0f} TFLOP/s)")
 
-    # --- policy none on the gated policies' kernel (descriptor instantiation,
+    # policy none on the gated policies' kernel (descriptor instantiation,
     # empty table): separates the arena's own effect from the instantiation's
-    same_ms = same_kernel_pass(data, empty_table_launcher(torch, api, workloads, cfg, stream))
+    same_ms = alone[SAME_KERNEL]
     same_out = torch.empty_like(data[0][3])
-    empty_table_launcher(torch, api, workloads, cfg, stream)(*data[0][:3], same_out)
+    same_launch(*data[0][:3], same_out)
     torch.cuda.synchronize()
     tf = fl_layer / (same_ms * 1e-3) / 1e12
     rec = {"what": "policy none through the descriptor instantiation with an empty table "
