@@ -16,6 +16,9 @@ be bitwise that of the same launch reading the map alone
   equals the oracle's attention with those rows replaced, and the map-only
   launch bit for bit;
 * a table of "general" entries only (every group decoded from the map);
+* an empty table (every map entry -1, every descriptor "no arena row"):
+  bitwise the map-free launch at the c3, c4 and c5 layer shapes, which is
+  what lets bench.py time and count policy none through this kernel;
 * the frame pipeline (kvp_pipeline_run, which writes the tables in its
   staging launch): device tables equal kvp_attn_group_desc over the device
   map slices after each of three layers, and the pipeline output equals
@@ -210,6 +213,28 @@ def test_all_general_table_equals_map_launch():
     got_gd = _launch(qd, kd, vd, frames, T, heads, "cross", 0, ad, md, full, gd)
     got_map = _launch(qd, kd, vd, frames, T, heads, "cross", 0, ad, md, full)
     assert torch.equal(got_gd, got_map)
+
+
+@pytest.mark.parametrize("frames,T,window", [(8, 1560, 0), (12, 1560, 8), (21, 3600, 0)])
+def test_empty_table_equals_map_free_launch(frames, T, window):
+    """Policy none through the descriptor launch (every map entry -1, every
+    descriptor entry "no arena row", a one-row arena never read) is bitwise
+    the map-free launch, at the layer shapes of the c3, c4 (fewer frames,
+    same window) and c5 workloads."""
+    print(f"empty table frames={frames} T={T} window={window}", flush=True)
+    heads = workloads.HEADS
+    D = workloads.HIDDEN
+    q, k, v = workloads.qkv_device(frames, T, seed=frames + window, dtype=torch.bfloat16)
+    span = frames * T
+    longest = (min(window, frames) if window else frames) * T
+    n = 4 * ((longest + 63) // 64)
+    kvmap = torch.full((frames * span,), -1, dtype=torch.int64, device=DEV)
+    gd = np.zeros((frames, n, 2), dtype=np.uint32)
+    arena = torch.zeros((1, 2 * D), dtype=torch.bfloat16, device=DEV)
+    free = _launch(q, k, v, frames, T, heads, "cross", window)
+    empty = _launch(q, k, v, frames, T, heads, "cross", window, arena, kvmap, span, gd)
+    assert torch.equal(free, empty)
+    assert bool(torch.isfinite(free).all())
 
 
 def _d2h(ptr, nbytes):
