@@ -1149,7 +1149,14 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_bf16_kernel(AttnArgs a) 
         for (int t = 0; t < ntiles; ++t) {
             unsigned char* kcur = (t & 1) ? k_lds1 : k_lds0;
             unsigned char* vcur = (t & 1) ? v_lds1 : v_lds0;
-            wait_vm<0>();
+            // The newest vector-memory operation of the wave is the
+            // descriptor load issued at the end of the previous step (used
+            // one step later); everything before it -- this tile's copies and
+            // overwrites -- has landed once at most one is outstanding (a
+            // wave's vector-memory operations complete in issue order).
+            // Waiting for all of them would expose that load's latency on
+            // every tile.
+            wait_vm<1>();
             wg_barrier();
             if (active) {
                 compute_tile(tix(t), kcur, vcur, [&](int ks) {
