@@ -442,18 +442,59 @@ __global__ __launch_bounds__(kPThreads, 2) void proj_gemm_bf16_small_kernel(Proj
     }
 
     const int nk = a.K / kPChunkK;
+    constexpr int kFeat = TN / 2;
+    constexpr int kEs = (int)sizeof(OutT);
+    constexpr int kChunks = kFeat * kEs / 16;
+    constexpr int kRowsPerPass = 64 / kChunks;
+    constexpr int kPasses = 32 / kRowsPerPass;
+    OutT* out = static_cast<OutT*>(a.out[g]);
+    const int rchunk = lane % kChunks;
+    const int rrow = lane / kChunks;
+    // Accumulating (out_proj into the fp32 residual stream): every residual
+    // value the wave adds in the epilogue, loaded all at once during the last
+    // chunk's MFMAs (issued after the copies of that chunk, one chunk ahead),
+    // so that their memory latency is not paid at the end of every tile.
+    float4 resid[kAcc ? JR : 1][kAcc ? kPasses : 1];
+    auto load_resid = [&]() {
+#pragma unroll
+        for (int j = 0; j < JR; ++j) {
+#pragma unroll
+            for (int pass = 0; pass < kPasses; ++pass) {
+                const long r = r0 + wr * (TR / 2) + 32 * j + pass * kRowsPerPass + rrow;
+                // every lane loads (a row past the end reads the last row; the
+                // epilogue never writes such rows), so the loop's wait below
+                // counts exactly these JR * kPasses loads
+                const long rc = r < a.rows ? r : a.rows - 1;
+                const float* gp = reinterpret_cast<const float*>(out) + rc * a.Ng + n0 +
+                                  wn * kFeat + 4 * rchunk;
+                resid[j][pass] = *reinterpret_cast<const float4*>(gp);
+            }
+        }
+    };
 #pragma unroll
     for (int c = 0; c < kCP; ++c) issue_copy(c, 0, 0u);
     u32x4 fr[2][NF];
     for (int t = 0; t < nk; ++t) {
         const int st = t & 1;
         // chunk t has landed for every wave after the barrier, and every
-        // wave has finished chunk t-1, whose stage the next copies refill
-        pj_wait_vm0();
+        // wave has finished chunk t-1, whose stage the next copies refill.
+        // Before the last chunk, the only loads issued after chunk t's copies
+        // are the residual loads (a wave's vector-memory operations complete
+        // in issue order), which may stay in flight.
+        if (kAcc && t == nk - 1 && nk >= 2)
+            asm volatile("s_waitcnt vmcnt(%0)" ::"n"(JR * kPasses) : "memory");
+        else
+            pj_wait_vm0();
         pj_barrier();
         if (t + 1 < nk) {
 #pragma unroll
             for (int c = 0; c < kCP; ++c) issue_copy(c, st ^ 1, (unsigned)(t + 1) * kPRowBytes);
+        }
+        if constexpr (kAcc) {
+            if (t == nk - 2) {
+                asm volatile("" ::: "memory");  // the loads go out after the copies
+                load_resid();
+            }
         }
         read_frags(fr[0], st, 0);
 #pragma unroll
@@ -474,34 +515,10 @@ __global__ __launch_bounds__(kPThreads, 2) void proj_gemm_bf16_small_kernel(Proj
     }
 
     // epilogue: as in the large-tile kernel, 32 tokens at a time
-    constexpr int kFeat = TN / 2;
-    constexpr int kEs = (int)sizeof(OutT);
     constexpr int kRowB = kFeat * kEs + 16;
-    constexpr int kChunks = kFeat * kEs / 16;
-    constexpr int kRowsPerPass = 64 / kChunks;
     static_assert(4 * 32 * kRowB <= 2 * kSB, "staging exceeds LDS");
-    OutT* out = static_cast<OutT*>(a.out[g]);
-    const int rchunk = lane % kChunks;
-    const int rrow = lane / kChunks;
-    // Accumulating (out_proj into the fp32 residual stream): every residual
-    // value the wave adds is loaded first, all at once, so the loads overlap
-    // one another and the staging below (loaded pass by pass, each add waited
-    // for its own load: 2 x 8 round trips to memory per wave at the end of
-    // every tile).
-    constexpr int kPasses = 32 / kRowsPerPass;
-    float4 resid[kAcc ? JR : 1][kAcc ? kPasses : 1];
     if constexpr (kAcc) {
-#pragma unroll
-        for (int j = 0; j < JR; ++j) {
-#pragma unroll
-            for (int pass = 0; pass < kPasses; ++pass) {
-                const long r = r0 + wr * (TR / 2) + 32 * j + pass * kRowsPerPass + rrow;
-                const float* gp = reinterpret_cast<const float*>(out) + r * a.Ng + n0 +
-                                  wn * kFeat + 4 * rchunk;
-                resid[j][pass] = r < a.rows ? *reinterpret_cast<const float4*>(gp)
-                                            : make_float4(0.f, 0.f, 0.f, 0.f);
-            }
-        }
+        if (nk < 2) load_resid();  // a one-chunk K: no earlier chunk to load under
     }
     pj_barrier();
     unsigned char* sbase = lds + wave * 32 * kRowB;
