@@ -600,10 +600,17 @@ void launch_small(const ProjArgs& a, hipStream_t st) {
 // each chunk of w and x is staged in LDS as 64 rows of 32 values padded to
 // 33, so that the 32 lanes of a half-wave reading one k of 32 rows hit 32
 // distinct banks. Every global access is bounds-checked: any rows, K and N.
+// The epilogue stages the 64 x 64 tile in the same LDS as rows (pitch 65)
+// and stores it row by row, 16 lanes per 64-value row, 4 consecutive values
+// per lane (one 16-byte fp32 / 8-byte bf16 store where the row and its
+// alignment allow, per-value stores at ragged edges): a row's 256 bytes go
+// out together instead of 4-byte pieces of 32 rows per instruction.
 // ---------------------------------------------------------------------------
 constexpr int kGTile = 64;
 constexpr int kGChunk = 32;
 constexpr int kGPitch = kGChunk + 1;
+constexpr int kGOutPitch = kGTile + 1;
+static_assert(kGTile * kGOutPitch <= 2 * kGTile * kGPitch, "output staging exceeds LDS");
 
 struct GenericArgs {
     const void* x;
@@ -622,8 +629,9 @@ __device__ __forceinline__ float to_f32(T v) {
 
 template <typename InT, typename OutT, bool kAcc>
 __global__ __launch_bounds__(256) void gemm_generic_kernel(GenericArgs a) {
-    __shared__ float ws[kGTile * kGPitch];
-    __shared__ float xs[kGTile * kGPitch];
+    __shared__ float lds[2 * kGTile * kGPitch];
+    float* ws = lds;
+    float* xs = lds + kGTile * kGPitch;
     const int tid = threadIdx.x;
     const int wave = tid >> 6;
     const int lane = tid & 63;
@@ -661,16 +669,58 @@ __global__ __launch_bounds__(256) void gemm_generic_kernel(GenericArgs a) {
         }
         __syncthreads();
     }
-    const long r = r0 + br + lr;
-    if (r >= a.rows) return;
-    OutT* Y = static_cast<OutT*>(a.y) + r * a.N;
+    // stage: row br + lr of the tile, columns bn + 8*(v/4) + 4*lk + v%4
+    // (the loop's last barrier has freed the operand tiles)
 #pragma unroll
     for (int v = 0; v < 16; ++v) {
-        const long n = n0 + bn + 8 * (v / 4) + 4 * lk + v % 4;
-        if (n >= a.N) continue;
-        float val = acc[v] + (a.bias ? a.bias[n] : 0.f);
-        if constexpr (kAcc) val += to_f32(Y[n]);
-        Y[n] = (OutT)val;
+        const int col = bn + 8 * (v / 4) + 4 * lk + v % 4;
+        const long n = n0 + col;
+        lds[(br + lr) * kGOutPitch + col] = acc[v] + (a.bias && n < a.N ? a.bias[n] : 0.f);
+    }
+    __syncthreads();
+    // 64 rows x 16 four-value groups, 4 per thread; 16 consecutive threads
+    // cover one row
+    const bool vec_ok = (a.N % 4) == 0 &&
+                        ((uintptr_t)a.y % (4 * sizeof(OutT))) == 0;
+#pragma unroll
+    for (int j = 0; j < kGTile * kGTile / 4 / 256; ++j) {
+        const int c = tid + 256 * j;
+        const int row = c / (kGTile / 4);
+        const int col = 4 * (c % (kGTile / 4));
+        const long r = r0 + row;
+        const long n = n0 + col;
+        if (r >= a.rows || n >= a.N) continue;
+        const float* src = lds + row * kGOutPitch + col;
+        OutT* Y = static_cast<OutT*>(a.y) + r * a.N + n;
+        if (vec_ok) {
+            // n + 3 < N: N and n are multiples of 4
+            float v4[4] = {src[0], src[1], src[2], src[3]};
+            if constexpr (sizeof(OutT) == 4) {
+                if constexpr (kAcc) {
+                    const float4 y = *reinterpret_cast<const float4*>(Y);
+                    v4[0] += y.x;
+                    v4[1] += y.y;
+                    v4[2] += y.z;
+                    v4[3] += y.w;
+                }
+                *reinterpret_cast<float4*>(Y) = make_float4(v4[0], v4[1], v4[2], v4[3]);
+            } else {
+                struct alignas(8) B4 {
+                    OutT v[4];
+                } o;
+#pragma unroll
+                for (int i = 0; i < 4; ++i) o.v[i] = (OutT)v4[i];
+                *reinterpret_cast<B4*>(Y) = o;
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                if (n + i >= a.N) break;
+                float val = src[i];
+                if constexpr (kAcc) val += to_f32(Y[i]);
+                Y[i] = (OutT)val;
+            }
+        }
     }
 }
 
