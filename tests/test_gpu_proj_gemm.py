@@ -33,6 +33,10 @@ CASES = [
     (1560, 1536, 1536, 3, 128, 1, False, False),
     (257, 128, 384, 2, 128, 0, False, True),
     (1000, 1536, 1536, 1, 256, 0, True, True),
+    # accumulate form, K of one chunk (residual loaded in the epilogue) and of
+    # two (loaded during the first), ragged last row tile
+    (130, 64, 128, 1, 128, 0, True, True),
+    (257, 128, 256, 1, 128, 0, True, False),
     (1560, 1536, 1536, 1, 128, 0, True, True),
     (12480, 1536, 1536, 3, 256, 1, False, True),
     (12480, 1536, 1536, 3, 128, 1, False, True),
