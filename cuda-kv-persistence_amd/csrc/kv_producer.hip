@@ -107,12 +107,17 @@ __global__ __launch_bounds__(64 * kLnRowsPerBlock) void layer_norm_kernel(
     if (row >= rows) return;
     const InT* xr = x + row * (long)D;
     float v[NCH][4];
+    // gamma and beta are loaded with the row, so that the only memory round
+    // trip before the stores is the row's own
+    float g[NCH][4], b[NCH][4];
     float s = 0.f;
 #pragma unroll
     for (int c = 0; c < NCH; ++c) {
         const int col = c * 256 + lane * 4;
         if (col < D) {
             load4(xr + col, v[c]);
+            load4(gamma + col, g[c]);
+            load4(beta + col, b[c]);
             s += (v[c][0] + v[c][1]) + (v[c][2] + v[c][3]);
         } else {
             v[c][0] = v[c][1] = v[c][2] = v[c][3] = 0.f;
@@ -138,11 +143,9 @@ __global__ __launch_bounds__(64 * kLnRowsPerBlock) void layer_norm_kernel(
     for (int c = 0; c < NCH; ++c) {
         const int col = c * 256 + lane * 4;
         if (col < D) {
-            float g[4], b[4], o[4];
-            load4(gamma + col, g);
-            load4(beta + col, b);
+            float o[4];
 #pragma unroll
-            for (int e = 0; e < 4; ++e) o[e] = fmaf((v[c][e] - mean) * rstd, g[e], b[e]);
+            for (int e = 0; e < 4; ++e) o[e] = fmaf((v[c][e] - mean) * rstd, g[c][e], b[c][e]);
             store4(yr + col, o);
         }
     }
