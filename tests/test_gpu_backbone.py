@@ -146,6 +146,39 @@ def test_linear_matches_oracle(in_dt, out_dt, acc, rows, K, N, bias):
         _bf16_close(got, want, "linear bf16")
 
 
+@pytest.mark.gpu
+@pytest.mark.parametrize("out_dt,acc", [(0, False), (0, True), (1, False)])
+def test_linear_output_off_the_16_byte_grid(out_dt, acc):
+    """The generic kernel stores whole-row 16-byte (8-byte for bf16) pieces
+    only where the output allows them; an output one element off that grid
+    takes the per-value stores, with the same result and nothing written
+    outside it."""
+    rows, K, N = 70, 48, 200
+    in_dt = 1 if out_dt == 1 else 0
+    rng = np.random.default_rng(7)
+    x = rng.standard_normal((rows, K)).astype(np.float32)
+    w = (0.02 * rng.standard_normal((N, K))).astype(np.float32)
+    if in_dt == 1:
+        x, w = ob.round_bf16(x), ob.round_bf16(w)
+    b = (0.1 * rng.standard_normal(N)).astype(np.float32)
+    y0 = rng.standard_normal(rows * N + 2).astype(np.float32)
+    if out_dt == 1:
+        y0 = ob.round_bf16(y0)
+    buf = torch.from_numpy(y0).to(DEV).to(TDT[out_dt])
+    y = buf[1:1 + rows * N].view(rows, N)
+    kb.linear(torch.from_numpy(x).to(DEV).to(TDT[in_dt]), torch.from_numpy(w).to(DEV).to(TDT[in_dt]),
+              torch.from_numpy(b).to(DEV), y, accumulate=acc)
+    torch.cuda.synchronize()
+    full = buf.float().cpu().numpy()
+    assert full[0] == y0[0] and full[-1] == y0[-1], "wrote outside the output"
+    want = ob.linear(x, w, b) + (y0[1:1 + rows * N].reshape(rows, N) if acc else 0)
+    got = full[1:1 + rows * N].reshape(rows, N)
+    if out_dt == 0:
+        assert _err(got, want)[0] <= 1e-4
+    else:
+        _bf16_close(got, want, "linear bf16, off-grid output")
+
+
 # ------------------------------------------------------------------ qkv projection
 
 def _params_from(model):
